@@ -1,0 +1,211 @@
+/* kurumi_hip C ABI: the MI355X (gfx950) backend for kurumi graphs.
+ *
+ * The graph-builder, eval, feeds, tensor, inspection and plan entry points keep the names,
+ * argument meaning and error conventions of the reference header
+ * (reference: kurumi/include/kurumi.h; each prototype below cites the line it mirrors), so a
+ * frontend written against kurumi.h links against libkurumi_hip.so unchanged for this subset.
+ * Conventions: builders return a node id or KU_ERR (then ku_last_error()); pointer-returning
+ * calls return NULL on error; int-returning calls return 0 / -1. Handles are opaque and freed
+ * with their ku_*_free. Not thread-safe per handle (kurumi.h:5).
+ *
+ * Backend kinds: KU_CPU (0) is the reference interpreter and lives in kurumi itself; this
+ * library provides KU_HIP (2) only. Every op a KU_HIP backend accepts runs on the GPU; an op
+ * outside its scope makes eval fail with an error (there is no CPU fallback).
+ *
+ * Entry points prefixed ku_hip_ have no counterpart in kurumi.h: device-resident plans for
+ * benchmarking/serving, profile counters and codegen introspection. */
+#ifndef KURUMI_HIP_H
+#define KURUMI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KU_ERR 0xFFFFFFFFu /* kurumi.h:25 */
+
+/* kurumi.h:29-34 (index = kurumi DType declaration order) */
+typedef enum {
+  KU_BOOL = 0, KU_U8, KU_U16, KU_U32, KU_U64,
+  KU_I8, KU_I16, KU_I32, KU_I64,
+  KU_F8E4M3, KU_F8E5M2, KU_F16, KU_BF16, KU_F32, KU_F64,
+  KU_C64, KU_C128
+} KuDType;
+
+/* kurumi.h:38, plus KU_HIP */
+typedef enum { KU_CPU = 0, KU_METAL = 1, KU_HIP = 2 } KuBackendKind;
+
+typedef struct KuGraph KuGraph;
+typedef struct KuTensor KuTensor;
+typedef struct KuFeeds KuFeeds;
+typedef struct KuBackend KuBackend;
+typedef struct KuPlan KuPlan;
+typedef struct KuHipPlan KuHipPlan;
+typedef uint32_t KuNode;
+
+const char *ku_last_error(void); /* kurumi.h:51 */
+
+/* graph lifecycle and leaves: kurumi.h:54-60 */
+KuGraph *ku_graph_new(void);
+void ku_graph_free(KuGraph *g);
+KuNode ku_input(KuGraph *g, const size_t *shape, size_t rank, uint32_t dtype);
+KuNode ku_constant_f32(KuGraph *g, const float *data, size_t len, const size_t *shape, size_t rank);
+KuNode ku_constant(KuGraph *g, uint32_t dtype, const uint8_t *data, size_t nbytes, const size_t *shape, size_t rank);
+KuNode ku_scalar(KuGraph *g, KuNode like, float v);
+
+/* two-operand builders: kurumi.h:63-80 */
+KuNode ku_add(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_sub(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_mul(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_div(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_max(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_idiv(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_and(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_or(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_xor(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_shl(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_shr(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_lt(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_eq(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_where(KuGraph *g, KuNode cond, KuNode a, KuNode b); /* kurumi.h:244 */
+
+/* unary builders: kurumi.h:101-127 */
+KuNode ku_neg(KuGraph *g, KuNode x);
+KuNode ku_recip(KuGraph *g, KuNode x);
+KuNode ku_sqrt(KuGraph *g, KuNode x);
+KuNode ku_square(KuGraph *g, KuNode x);
+KuNode ku_abs(KuGraph *g, KuNode x);
+KuNode ku_floor(KuGraph *g, KuNode x);
+KuNode ku_exp(KuGraph *g, KuNode x);
+KuNode ku_exp2(KuGraph *g, KuNode x);
+KuNode ku_ln(KuGraph *g, KuNode x);
+KuNode ku_log2(KuGraph *g, KuNode x);
+KuNode ku_sin(KuGraph *g, KuNode x);
+KuNode ku_cos(KuGraph *g, KuNode x);
+KuNode ku_relu(KuGraph *g, KuNode x);
+KuNode ku_flatten(KuGraph *g, KuNode x); /* kurumi.h:160 */
+KuNode ku_t(KuGraph *g, KuNode x);       /* kurumi.h:161 */
+KuNode ku_sum_all(KuGraph *g, KuNode x); /* kurumi.h:165 */
+
+/* reductions over one axis: kurumi.h:186-199 */
+KuNode ku_sum(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_prod(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_mean(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_reduce_max(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_argmax(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_argmin(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_softmax(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_squeeze(KuGraph *g, KuNode x, size_t axis);   /* kurumi.h:209 */
+KuNode ku_unsqueeze(KuGraph *g, KuNode x, size_t axis); /* kurumi.h:210 */
+KuNode ku_clamp_min(KuGraph *g, KuNode x, float v);     /* kurumi.h:217 */
+KuNode ku_rmsnorm(KuGraph *g, KuNode x, size_t axis, float eps); /* kurumi.h:302 */
+
+/* contraction: kurumi.h:221-224 */
+KuNode ku_matmul(KuGraph *g, KuNode a, KuNode b);
+KuNode ku_dot_general(KuGraph *g, KuNode a, KuNode b, const size_t *lc, size_t nlc, const size_t *rc, size_t nrc,
+                      const size_t *lb, size_t nlb, const size_t *rb, size_t nrb);
+
+/* movement: kurumi.h:269-276, 286-292 */
+KuNode ku_reshape(KuGraph *g, KuNode x, const size_t *shape, size_t rank);
+KuNode ku_expand(KuGraph *g, KuNode x, const size_t *shape, size_t rank);
+KuNode ku_permute(KuGraph *g, KuNode x, const size_t *perm, size_t rank);
+KuNode ku_transpose(KuGraph *g, KuNode x, size_t i, size_t j);
+KuNode ku_flip(KuGraph *g, KuNode x, const size_t *axes, size_t n);
+KuNode ku_slice(KuGraph *g, KuNode x, const size_t *ranges, size_t rank);      /* 2*rank (start,end) */
+KuNode ku_slice_step(KuGraph *g, KuNode x, const size_t *ranges, size_t rank); /* 3*rank (start,end,step) */
+KuNode ku_pad(KuGraph *g, KuNode x, const size_t *pads, size_t rank);          /* 2*rank (lo,hi), 0 */
+KuNode ku_broadcast_to(KuGraph *g, KuNode x, const size_t *shape, size_t rank);
+KuNode ku_detach(KuGraph *g, KuNode x);
+KuNode ku_iota(KuGraph *g, const size_t *shape, size_t rank, size_t axis, uint32_t dtype);
+KuNode ku_cast(KuGraph *g, KuNode x, uint32_t dtype);
+KuNode ku_bitcast(KuGraph *g, KuNode x, uint32_t dtype);
+
+/* attention: kurumi.h:343 (auto-selects fused vs decomposed like the reference builder) */
+KuNode ku_sdpa(KuGraph *g, KuNode q, KuNode k, KuNode v, uint32_t causal);
+/* random: kurumi.h:346-350 */
+KuNode ku_rand_uniform(KuGraph *g, const size_t *shape, size_t rank, uint64_t seed);
+KuNode ku_randn(KuGraph *g, const size_t *shape, size_t rank, uint64_t seed);
+KuNode ku_rand_range(KuGraph *g, const size_t *shape, size_t rank, uint64_t seed, float lo, float hi);
+
+/* backend + eval: kurumi.h:381-388 */
+KuBackend *ku_backend_new(uint32_t kind); /* NULL if unavailable */
+void ku_backend_free(KuBackend *b);
+KuTensor *ku_eval(KuGraph *g, KuNode node, const KuBackend *backend);
+KuTensor *ku_eval_with(KuGraph *g, KuNode node, const KuBackend *backend, const KuFeeds *feeds);
+int32_t ku_eval_many(KuGraph *g, const KuNode *ids, size_t n, const KuBackend *backend, const KuFeeds *feeds,
+                     KuTensor **out);
+
+/* inspection: kurumi.h:396-405 */
+size_t ku_node_count(const KuGraph *g, KuNode root);
+size_t ku_dump(const KuGraph *g, KuNode root, uint8_t *out, size_t cap);
+size_t ku_node_rank(const KuGraph *g, KuNode node);
+void ku_node_shape(const KuGraph *g, KuNode node, size_t *out);
+uint32_t ku_node_dtype(const KuGraph *g, KuNode node);
+
+/* plan-replay: kurumi.h:456-458. Here the plan is a device plan on the process's default
+ * KU_HIP backend (device 0), replayed as one hipGraph launch per run. */
+KuPlan *ku_plan_compile(const KuGraph *g, KuNode node);
+KuTensor *ku_plan_run(const KuPlan *p, const KuGraph *g, const KuFeeds *feeds);
+void ku_plan_free(KuPlan *p);
+
+/* feeds: kurumi.h:461-463 */
+KuFeeds *ku_feeds_new(void);
+void ku_feeds_free(KuFeeds *f);
+void ku_feeds_set(KuFeeds *f, KuNode node, const KuTensor *tensor);
+
+/* tensors: kurumi.h:466-479 */
+KuTensor *ku_tensor_f32(const float *data, size_t len, const size_t *shape, size_t rank);
+KuTensor *ku_tensor_new(uint32_t dtype, const uint8_t *data, size_t nbytes, const size_t *shape, size_t rank);
+void ku_tensor_free(KuTensor *t);
+size_t ku_tensor_rank(const KuTensor *t);
+void ku_tensor_shape(const KuTensor *t, size_t *out);
+size_t ku_tensor_len(const KuTensor *t);
+uint32_t ku_tensor_dtype(const KuTensor *t);
+ptrdiff_t ku_tensor_data_f32(const KuTensor *t, float *out, size_t cap);
+size_t ku_tensor_nbytes(const KuTensor *t);
+void ku_tensor_bytes(const KuTensor *t, uint8_t *out);
+
+/* ---- extensions without a kurumi.h counterpart ---- */
+
+/* Explicit attention forms of the reference builders Graph::sdpa_decomposed / sdpa_fused
+ * (kurumi_core/src/graph/ops/nn/attention.rs:97-133), which kurumi.h does not export. */
+KuNode ku_sdpa_decomposed(KuGraph *g, KuNode q, KuNode k, KuNode v, uint32_t causal);
+KuNode ku_sdpa_fused(KuGraph *g, KuNode q, KuNode k, KuNode v, uint32_t causal);
+
+/* fp8 (OCP e4m3) mixed-precision pass: rewrites linear DotGenerals under `root` into a
+ * per-tensor-scaled activation x per-row-scaled weight e4m3 contraction (the e4m3 policy
+ * next to kurumi.h:395 ku_amp, which is f16-only). Returns the new root or KU_ERR. */
+KuNode ku_amp_fp8(KuGraph *g, KuNode root);
+
+/* Device-resident plan: compile `roots`, upload `feeds` once, then launch repeatedly with
+ * inputs and outputs staying in HBM. The graph must outlive the plan. */
+KuHipPlan *ku_hip_plan_new(KuGraph *g, const KuNode *roots, size_t n, const KuBackend *backend,
+                           const KuFeeds *feeds);
+int32_t ku_hip_plan_feed(KuHipPlan *p, KuNode input, const KuTensor *t);
+int32_t ku_hip_plan_launch(KuHipPlan *p, uint32_t use_graph); /* async on the backend stream */
+int32_t ku_hip_plan_sync(KuHipPlan *p);
+KuTensor *ku_hip_plan_output(KuHipPlan *p, size_t i);
+size_t ku_hip_plan_num_steps(const KuHipPlan *p);
+/* NUL-terminated label of step i (kernel name / variant); copied into out (cap bytes). */
+size_t ku_hip_plan_step_label(const KuHipPlan *p, size_t i, char *out, size_t cap);
+/* Average GPU milliseconds of each step over `iters` runs (hipEvents on the stream). */
+int32_t ku_hip_plan_time_steps(KuHipPlan *p, int32_t iters, double *out_ms, size_t cap);
+/* Average GPU milliseconds of a whole plan launch over `iters` runs. */
+double ku_hip_plan_time(KuHipPlan *p, int32_t iters, uint32_t use_graph);
+void ku_hip_plan_free(KuHipPlan *p);
+
+/* Generated HIP source of every fused region kernel for `roots`, concatenated and
+ * separated by a line "// ----"; works without a GPU (hipRTC compiles each for gfx950 when
+ * compile != 0). Returns the byte length; copies at most cap bytes into out. */
+size_t ku_hip_codegen(KuGraph *g, const KuNode *roots, size_t n, uint32_t compile, uint8_t *out, size_t cap);
+
+/* Dispatch counters of a backend: launches per kind (fused, gemm, attention, upload,
+ * download) into out[0..5]; returns the number of evals. */
+uint64_t ku_hip_profile(const KuBackend *b, uint64_t *out_launches, size_t cap);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* KURUMI_HIP_H */

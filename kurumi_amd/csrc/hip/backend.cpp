@@ -1,0 +1,61 @@
+#include "backend.h"
+
+namespace ku::hipbk {
+
+namespace {
+constexpr size_t kMaxCachedPlans = 8;
+}
+
+HipBackend::HipBackend(int device) {
+  ctx_ = std::make_unique<Context>(device);
+  consts_ = std::make_unique<ConstCache>(ctx_.get());
+}
+
+HipBackend::~HipBackend() {
+  plans_.clear();
+  consts_.reset();
+  ctx_.reset();
+}
+
+std::unique_ptr<Plan> HipBackend::new_plan(const Graph& g, const std::vector<NodeId>& roots) {
+  ctx_->make_current();
+  return std::make_unique<Plan>(g, roots, ctx_.get(), consts_.get());
+}
+
+std::shared_ptr<Plan> HipBackend::plan_for(const Graph& g, const std::vector<NodeId>& roots) {
+  for (auto it = plans_.begin(); it != plans_.end(); ++it) {
+    if (it->gid == g.id() && it->gsize == g.size() && it->roots == roots) {
+      if (it != plans_.begin()) plans_.splice(plans_.begin(), plans_, it);
+      return plans_.front().plan;
+    }
+  }
+  std::shared_ptr<Plan> p(new_plan(g, roots).release());
+  plans_.push_front(Entry{g.id(), g.size(), roots, p});
+  while (plans_.size() > kMaxCachedPlans) plans_.pop_back();
+  return p;
+}
+
+void feed_plan(Plan& p, const Feeds& feeds) {
+  for (NodeId in : p.inputs()) {
+    auto it = feeds.find(in);
+    if (it == feeds.end()) throw Error("eval: missing feed for Input node %" + std::to_string(in));
+    p.feed(in, *it->second);
+  }
+}
+
+// Mirrors MetalBackend::eval_many_with (kurumi_metal/src/backend.rs:95-109): one shared
+// pass over all ids, results downloaded as owned host tensors.
+std::vector<Tensor> HipBackend::eval_many(const Graph& g, const std::vector<NodeId>& ids, const Feeds& feeds) {
+  if (ids.empty()) return {};
+  ctx_->make_current();
+  std::shared_ptr<Plan> p = plan_for(g, ids);
+  feed_plan(*p, feeds);
+  p->launch(false);
+  std::vector<Tensor> out;
+  out.reserve(ids.size());
+  for (size_t i = 0; i < ids.size(); ++i) out.push_back(p->download(i));
+  ctx_->profile().evals++;
+  return out;
+}
+
+}  // namespace ku::hipbk

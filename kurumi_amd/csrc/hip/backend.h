@@ -1,0 +1,42 @@
+// HipBackend: the MI355X implementation of the backend seam
+// (kurumi_core/src/backend.rs:14-31; the Metal analog is kurumi_metal/src/backend.rs:19-109).
+// Every op it accepts runs on the device; an op outside its scope is an error, never a
+// silent CPU fallback.
+#pragma once
+#include <list>
+#include <memory>
+
+#include "../ir/tensor.h"
+#include "plan.h"
+#include "runtime.h"
+
+namespace ku::hipbk {
+
+class HipBackend : public ku::Backend {
+ public:
+  explicit HipBackend(int device);
+  ~HipBackend() override;
+  const char* name() const override { return "hip"; }
+  std::vector<Tensor> eval_many(const Graph& g, const std::vector<NodeId>& ids, const Feeds& feeds) override;
+
+  // A device plan for `roots` (cached per graph id + roots + graph size).
+  std::shared_ptr<Plan> plan_for(const Graph& g, const std::vector<NodeId>& roots);
+  std::unique_ptr<Plan> new_plan(const Graph& g, const std::vector<NodeId>& roots);
+  Context& ctx() { return *ctx_; }
+  ConstCache& consts() { return *consts_; }
+
+ private:
+  std::unique_ptr<Context> ctx_;
+  std::unique_ptr<ConstCache> consts_;
+  struct Entry {
+    uint64_t gid;
+    size_t gsize;
+    std::vector<NodeId> roots;
+    std::shared_ptr<Plan> plan;
+  };
+  std::list<Entry> plans_;  // most recent first
+};
+
+void feed_plan(Plan& p, const Feeds& feeds);
+
+}  // namespace ku::hipbk

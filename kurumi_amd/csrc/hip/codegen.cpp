@@ -1,0 +1,775 @@
+// HIP source generation for line regions (kernel family 1: fused pointwise/reduce, and
+// family 3: the one-pass softmax with its argmax epilogue).
+//
+// A region iterates a shape S. Without a reduction axis it is a flat elementwise kernel
+// (each thread owns V consecutive elements, 128-bit loads/stores where the layout allows).
+// With an axis it is a line kernel: TPL threads own one line of S along the axis, hold
+// the line's loaded values in registers across phases, fold each reduction level with a
+// wave64 butterfly (+ an LDS combine across waves) and store every output in the same
+// pass. Per-primitive rounding of f16/bf16/fp8 values matches the oracle
+// (kurumi_core/src/dtype/traits/float.rs:8-72,132-161): each op computes in f32 and rounds.
+// Reductions of low-precision floats accumulate in f32 and round once
+// (interp/reduce.rs:89-106). ArgReduce keeps the oracle's first-index tie rule and its NaN
+// behaviour (interp/reduce.rs:18-65). The reference's Metal emitters this replaces are
+// kurumi_metal/src/backend/fuse/emit.rs:80-142.
+#include <algorithm>
+#include <cmath>
+#include <functional>
+#include <map>
+#include <set>
+#include <sstream>
+
+#include "device_prelude.h"
+#include "plan.h"
+
+namespace ku::hipbk {
+
+namespace {
+
+const char* stype(DType d) {  // storage type
+  switch (d) {
+    case DType::BOOL: case DType::U8: case DType::F8E4M3: case DType::F8E5M2: return "u8";
+    case DType::U16: case DType::F16: case DType::BF16: return "u16";
+    case DType::U32: return "u32";
+    case DType::U64: return "u64";
+    case DType::I8: return "i8";
+    case DType::I16: return "i16";
+    case DType::I32: return "i32";
+    case DType::I64: return "i64";
+    case DType::F32: return "float";
+    case DType::F64: return "double";
+    default: throw Error(std::string("kurumi_hip: dtype ") + dt_name(d) + " is not supported on device");
+  }
+}
+const char* ctype(DType d) {  // compute type
+  switch (d) {
+    case DType::BOOL: return "bool";
+    case DType::F8E4M3: case DType::F8E5M2: case DType::F16: case DType::BF16: case DType::F32: return "float";
+    case DType::F64: return "double";
+    default: return stype(d);
+  }
+}
+const char* utype(DType d) {  // unsigned twin for wrapping arithmetic
+  switch (d) {
+    case DType::U8: case DType::I8: return "u8";
+    case DType::U16: case DType::I16: return "u16";
+    case DType::U32: case DType::I32: return "u32";
+    case DType::U64: case DType::I64: return "u64";
+    default: return "u32";
+  }
+}
+int bits(DType d) { return (int)dt_width(d) * 8; }
+bool fvalued(DType d) { return d == DType::F32 || dt_is_lowp(d); }
+
+std::string ld(DType d, const std::string& raw) {
+  switch (d) {
+    case DType::BOOL: return "(" + raw + " != 0)";
+    case DType::F16: return "f16_ld(" + raw + ")";
+    case DType::BF16: return "bf16_ld(" + raw + ")";
+    case DType::F8E4M3: return "f8e4m3_ld(" + raw + ")";
+    case DType::F8E5M2: return "f8e5m2_ld(" + raw + ")";
+    default: return raw;
+  }
+}
+std::string st(DType d, const std::string& v) {
+  switch (d) {
+    case DType::BOOL: return "(u8)(" + v + ")";
+    case DType::F16: return "f16_st(" + v + ")";
+    case DType::BF16: return "bf16_st(" + v + ")";
+    case DType::F8E4M3: return "f8e4m3_st(" + v + ")";
+    case DType::F8E5M2: return "f8e5m2_st(" + v + ")";
+    default: return v;
+  }
+}
+std::string rnd(DType d, const std::string& v) {
+  switch (d) {
+    case DType::F16: return "rf16(" + v + ")";
+    case DType::BF16: return "rbf16(" + v + ")";
+    case DType::F8E4M3: return "rf8e4m3(" + v + ")";
+    case DType::F8E5M2: return "rf8e5m2(" + v + ")";
+    default: return v;
+  }
+}
+
+// cast with the reference's through-f64 semantics
+std::string cast_expr(DType from, DType to, const std::string& x) {
+  if (from == to) return x;
+  bool ffrom = fvalued(from);
+  std::string dx = "((double)(" + x + "))";
+  switch (to) {
+    case DType::F32:
+      if (ffrom) return x;
+      return "((float)" + dx + ")";
+    case DType::F64: return dx;
+    case DType::BF16: return ffrom ? "rbf16(" + x + ")" : "rbf16_d(" + dx + ")";
+    case DType::F16: return ffrom ? "rf16(" + x + ")" : "rf16_d(" + dx + ")";
+    case DType::F8E4M3: return ffrom ? "rf8e4m3(" + x + ")" : "rf8e4m3((float)" + dx + ")";
+    case DType::F8E5M2: return ffrom ? "rf8e5m2(" + x + ")" : "rf8e5m2((float)" + dx + ")";
+    case DType::BOOL: return "(" + dx + " != 0.0)";
+    default: return std::string("sat_int<") + stype(to) + ">(" + dx + ")";
+  }
+}
+
+std::string flt_lit(DType acc, double v) {
+  std::ostringstream o;
+  o.precision(17);
+  if (std::isinf(v)) return acc == DType::F64 ? (v > 0 ? "(double)INFINITY" : "(-(double)INFINITY)") : (v > 0 ? "INFINITY" : "(-INFINITY)");
+  o << v;
+  std::string s = o.str();
+  if (s.find_first_of(".e") == std::string::npos) s += ".0";
+  return acc == DType::F64 ? s : s + "f";
+}
+
+std::string int_min(DType d) {
+  switch (d) {
+    case DType::I8: return "(i8)-128";
+    case DType::I16: return "(i16)-32768";
+    case DType::I32: return "(i32)(-2147483647 - 1)";
+    case DType::I64: return "(i64)(-9223372036854775807ll - 1)";
+    default: return std::string("(") + stype(d) + ")0";
+  }
+}
+std::string int_max(DType d) {
+  switch (d) {
+    case DType::I8: return "(i8)127";
+    case DType::I16: return "(i16)32767";
+    case DType::I32: return "(i32)2147483647";
+    case DType::I64: return "(i64)9223372036854775807ll";
+    case DType::U8: return "(u8)255";
+    case DType::U16: return "(u16)65535";
+    case DType::U32: return "(u32)4294967295u";
+    case DType::U64: return "(u64)18446744073709551615ull";
+    default: return "0";
+  }
+}
+
+bool is_red(int k) {
+  return k == (int)OpKind::Sum || k == (int)OpKind::Prod || k == (int)OpKind::ReduceMax || k == (int)OpKind::ArgReduce;
+}
+
+struct Gen {
+  const Region& R;
+  const std::vector<Slot>& slots;
+  int index;
+  std::ostringstream o;
+  int rank = 0, a = -1;
+  bool flat = true;
+  int V = 1, TPL = 1, NC = 1, WG = 256, GPW = 1;
+  uint64_t lines = 1, L = 1, N = 1;
+  bool idx64 = false;
+  std::vector<int> param_slots;
+  std::map<int, int> slot_param;
+  std::vector<bool> leaf_vec;
+  int P = 0;  // reduction levels
+  std::vector<int> store_phase;    // per node: phase in which a FULL output is stored (0 none)
+  std::map<int, int> out_slot;     // rnode -> slot
+  std::vector<std::set<int>> need; // per phase (1..P+1): FULL nodes computed in that phase
+  std::set<int> cached;
+  std::vector<int> first_phase;    // per node: first phase computing it
+  bool has_final = false;
+  bool unroll = false;
+
+  Gen(const Region& r, const std::vector<Slot>& s, int i) : R(r), slots(s), index(i) {}
+
+  int param(int slot) {
+    auto it = slot_param.find(slot);
+    if (it != slot_param.end()) return it->second;
+    param_slots.push_back(slot);
+    slot_param[slot] = (int)param_slots.size() - 1;
+    return (int)param_slots.size() - 1;
+  }
+  const RNode& node(int i) const { return R.nodes[i]; }
+  bool full(int i) const { return R.nodes[i].space == Space::Full; }
+  std::string ix() const { return idx64 ? "u64" : "u32"; }
+
+  // value of node i at element j (FULL) or as a line scalar (LINE)
+  std::string val(int i, const std::string& j) const {
+    if (full(i)) return "f" + std::to_string(i) + "[" + j + "]";
+    return "s" + std::to_string(i);
+  }
+
+  std::string op_expr(int ni, const std::string& j) const;
+  void plan_layout();
+  void schedule();
+  void emit_leaf_load(int ni, const std::string& c_expr);
+  void emit_full_node(int ni, int phase, const std::string& c_expr);
+  void emit_line_node(int ni);
+  void emit_red_init(int ni);
+  void emit_red_update(int ni, const std::string& k_expr, const std::string& j);
+  void emit_red_finish(int ni, int phase);
+  std::string leaf_base(int leaf) const;
+  std::string generate(RegionCode* rc);
+};
+
+std::string Gen::op_expr(int ni, const std::string& j) const {
+  const RNode& n = node(ni);
+  DType d = n.dtype;
+  auto in = [&](int t) { return val(n.in[t], j); };
+  auto indt = [&](int t) { return node(n.in[t]).dtype; };
+  bool fl = fvalued(d), f64 = d == DType::F64;
+  std::string U = utype(d), T = stype(d);
+  switch (n.kind) {
+    case (int)OpKind::Add:
+      if (fl || f64) return rnd(d, "(" + in(0) + " + " + in(1) + ")");
+      return "(" + T + ")((" + U + ")" + in(0) + " + (" + U + ")" + in(1) + ")";
+    case (int)OpKind::Mul:
+      if (fl || f64) return rnd(d, "(" + in(0) + " * " + in(1) + ")");
+      return "(" + T + ")((" + U + ")" + in(0) + " * (" + U + ")" + in(1) + ")";
+    case (int)OpKind::Max:
+      if (fl) return "fmaxf(" + in(0) + ", " + in(1) + ")";
+      if (f64) return "fmax(" + in(0) + ", " + in(1) + ")";
+      return "(" + in(0) + " > " + in(1) + " ? " + in(0) + " : " + in(1) + ")";
+    case (int)OpKind::Neg:
+      if (fl || f64) return "(-" + in(0) + ")";
+      return "(" + T + ")(0 - (" + U + ")" + in(0) + ")";
+    case (int)OpKind::Recip: return f64 ? "(1.0 / " + in(0) + ")" : rnd(d, "(1.0f / " + in(0) + ")");
+    case (int)OpKind::Sqrt: return f64 ? "sqrt(" + in(0) + ")" : rnd(d, "sqrtf(" + in(0) + ")");
+    case (int)OpKind::Exp2: return f64 ? "exp2(" + in(0) + ")" : rnd(d, "exp2f(" + in(0) + ")");
+    case (int)OpKind::Log2: return f64 ? "log2(" + in(0) + ")" : rnd(d, "log2f(" + in(0) + ")");
+    case (int)OpKind::Sin: return f64 ? "sin(" + in(0) + ")" : rnd(d, "sinf(" + in(0) + ")");
+    case (int)OpKind::Floor: return f64 ? "floor(" + in(0) + ")" : rnd(d, "floorf(" + in(0) + ")");
+    case (int)OpKind::IDiv:
+      if (dt_is_unsigned(d)) return "(" + in(1) + " == 0 ? (" + T + ")0 : (" + T + ")(" + in(0) + " / " + in(1) + "))";
+      return "(" + in(1) + " == 0 ? (" + T + ")0 : (" + in(1) + " == -1 ? (" + T + ")(0 - (" + U + ")" + in(0) +
+             ") : (" + T + ")(" + in(0) + " / " + in(1) + ")))";
+    case (int)OpKind::And: return d == DType::BOOL ? "(" + in(0) + " && " + in(1) + ")" : "(" + T + ")(" + in(0) + " & " + in(1) + ")";
+    case (int)OpKind::Or: return d == DType::BOOL ? "(" + in(0) + " || " + in(1) + ")" : "(" + T + ")(" + in(0) + " | " + in(1) + ")";
+    case (int)OpKind::Xor: return d == DType::BOOL ? "(" + in(0) + " != " + in(1) + ")" : "(" + T + ")(" + in(0) + " ^ " + in(1) + ")";
+    case (int)OpKind::Shl:
+      return "(" + T + ")((" + U + ")" + in(0) + " << ((" + U + ")" + in(1) + " & " + std::to_string(bits(d) - 1) + "))";
+    case (int)OpKind::Shr:
+      return "(" + T + ")(" + in(0) + " >> ((" + U + ")" + in(1) + " & " + std::to_string(bits(d) - 1) + "))";
+    case (int)OpKind::CmpLt: return "(" + in(0) + " < " + in(1) + ")";
+    case (int)OpKind::CmpEq: return "(" + in(0) + " == " + in(1) + ")";
+    case (int)OpKind::Where: return "(" + in(0) + " ? " + in(1) + " : " + in(2) + ")";
+    case (int)OpKind::Cast: return cast_expr(indt(0), n.to, in(0));
+    case (int)OpKind::Bitcast: {
+      DType s = indt(0);
+      std::string raw = std::string("__builtin_bit_cast(") + stype(n.to) + ", (" + stype(s) + ")" + st(s, in(0)) + ")";
+      if (s == DType::BOOL || n.to == DType::BOOL) raw = std::string("(") + stype(n.to) + ")" + st(s, in(0));
+      return ld(n.to, raw);
+    }
+    case RK_DIV: return "(" + in(0) + " / " + in(1) + ")";
+    case RK_EXP: return f64 ? "exp(" + in(0) + ")" : "expf(" + in(0) + ")";
+    case RK_SQRT_ADD_EPS: {
+      std::string len = flt_lit(d, (double)n.axis), eps = flt_lit(d, (double)n.eps);
+      return f64 ? "sqrt(" + in(0) + " / " + len + " + " + eps + ")" : "sqrtf(" + in(0) + " / " + len + " + " + eps + ")";
+    }
+    default:
+      throw Error(std::string("kurumi_hip codegen: unsupported region op ") + op_name((OpKind)n.kind));
+  }
+}
+
+// Decide flat vs line layout, vector width, threads per line, chunks per thread.
+void Gen::plan_layout() {
+  rank = (int)R.S.size();
+  a = R.axis;
+  N = numel(R.S);
+  flat = a < 0;
+  size_t maxoff = N;
+  for (auto& l : R.leaves) {
+    int64_t hi = l.view.offset, lo = l.view.offset;
+    for (size_t d = 0; d < l.view.shape.size(); ++d) {
+      int64_t ext = (int64_t)(l.view.shape[d] ? l.view.shape[d] - 1 : 0) * l.view.strides[d];
+      if (ext > 0) hi += ext; else lo += ext;
+    }
+    maxoff = std::max<size_t>(maxoff, (size_t)std::max<int64_t>(hi, 0) + 1);
+    if (lo < 0) maxoff = std::max<size_t>(maxoff, (size_t)1 << 40);
+  }
+  idx64 = maxoff >= ((size_t)1 << 31);
+  int vecaxis = flat ? rank - 1 : a;
+  uint64_t inner = 1;
+  if (!flat)
+    for (int d = a + 1; d < rank; ++d) inner *= R.S[d];
+  L = flat ? R.S[rank - 1] : R.S[a];
+  lines = flat ? N / std::max<uint64_t>(L, 1) : N / std::max<uint64_t>(L, 1);
+  // vector width: 16 bytes of the narrowest streamed type, only along a contiguous last axis
+  int minw = 8;
+  bool contiguous_axis = flat || inner == 1;
+  for (auto& l : R.leaves)
+    if (l.view.strides[vecaxis] != 0) minw = std::min<int>(minw, (int)dt_width(l.dtype));
+  for (auto& op : R.outputs)
+    if (full(op.first) || flat) minw = std::min<int>(minw, (int)dt_width(node(op.first).dtype));
+  V = contiguous_axis ? std::min(8, 16 / std::max(minw, 1)) : 1;
+  while (V > 1 && (L % (uint64_t)V) != 0) V /= 2;
+  leaf_vec.assign(R.leaves.size(), false);
+  for (size_t i = 0; i < R.leaves.size(); ++i) {
+    const View& v = R.leaves[i].view;
+    bool ok = V > 1 && v.strides[vecaxis] == 1 && !v.padded() && (v.offset % V) == 0;
+    for (int d = 0; ok && d < rank; ++d)
+      if (d != vecaxis && (v.strides[d] % V) != 0) ok = false;
+    leaf_vec[i] = ok;
+  }
+  if (flat) {
+    TPL = 1;
+    WG = 256;
+    NC = 1;
+    return;
+  }
+  uint64_t chunks = (L + V - 1) / V;
+  if (inner > 1) {
+    TPL = 1;
+    WG = 256;
+    GPW = 256;
+    NC = (int)chunks;
+    return;
+  }
+  // multi-level programs keep lines in registers: aim at ~8 chunks per thread;
+  // single-level reductions stream: ~16 chunks per thread.
+  int target = 16;
+  for (auto& n : R.nodes)
+    if (n.level >= 2) target = 8;
+  uint64_t t = 1;
+  while (t < 1024 && t * (uint64_t)target < chunks) t *= 2;
+  TPL = (int)t;
+  NC = (int)((chunks + TPL - 1) / TPL);
+  WG = std::max(TPL, 256);
+  GPW = WG / TPL;
+}
+
+// Phases: level p = 1..P fold reductions of level p; LINE nodes of level p follow.
+// FULL outputs of level l are stored in phase l+1 (the final pass P+1 when l == P).
+void Gen::schedule() {
+  P = 0;
+  for (auto& n : R.nodes) P = std::max(P, n.level);
+  store_phase.assign(R.nodes.size(), 0);
+  for (auto& op : R.outputs) {
+    out_slot[op.first] = op.second;
+    if (full(op.first) || flat) {
+      int l = node(op.first).level;
+      store_phase[op.first] = l + 1;
+      if (l + 1 > P) has_final = true;
+    }
+  }
+  int nph = P + (has_final ? 1 : 0);
+  need.assign(nph + 2, {});
+  std::function<void(int, int)> add = [&](int p, int n) {
+    if (!full(n) || need[p].count(n)) return;
+    need[p].insert(n);
+    for (int i : node(n).in) add(p, i);
+  };
+  for (size_t i = 0; i < R.nodes.size(); ++i) {
+    const RNode& n = R.nodes[i];
+    if (is_red(n.kind)) add(n.level, n.in[0]);
+    if (store_phase[i]) add(store_phase[i], (int)i);
+  }
+  // cache leaves and reduction inputs that several phases need, when the line fits
+  first_phase.assign(R.nodes.size(), 0);
+  std::map<int, int> uses;
+  for (int p = 1; p <= nph; ++p)
+    for (int n : need[p]) {
+      uses[n]++;
+      if (!first_phase[n]) first_phase[n] = p;
+    }
+  std::set<int> red_inputs;
+  for (auto& n : R.nodes)
+    if (is_red(n.kind)) red_inputs.insert(n.in[0]);
+  unroll = !flat && NC <= 16;
+  if (!flat && NC <= 16) {
+    int regs = 0;
+    std::vector<int> cand;
+    for (auto& kv : uses)
+      if (kv.second >= 2 && (node(kv.first).kind == RK_LEAF || red_inputs.count(kv.first))) cand.push_back(kv.first);
+    for (int c : cand) regs += NC * V * (node(c).dtype == DType::F64 || dt_width(node(c).dtype) == 8 ? 2 : 1);
+    if (regs <= 160)
+      for (int c : cand) cached.insert(c);
+  }
+  // with caches, later phases need fewer recomputations: rebuild need sets
+  if (!cached.empty()) {
+    need.assign(nph + 2, {});
+    std::function<void(int, int)> add2 = [&](int p, int n) {
+      if (!full(n) || need[p].count(n)) return;
+      need[p].insert(n);
+      if (cached.count(n) && first_phase[n] < p) return;
+      for (int i : node(n).in) add2(p, i);
+    };
+    for (size_t i = 0; i < R.nodes.size(); ++i) {
+      const RNode& n = R.nodes[i];
+      if (is_red(n.kind)) add2(n.level, n.in[0]);
+      if (store_phase[i]) add2(store_phase[i], (int)i);
+    }
+  }
+}
+
+std::string Gen::leaf_base(int li) const {
+  const View& v = R.leaves[li].view;
+  int vecaxis = flat ? rank - 1 : a;
+  std::ostringstream e;
+  e << "(" << ix() << ")(" << v.offset << "ll";
+  for (int d = 0; d < rank; ++d) {
+    if (d == vecaxis || v.strides[d] == 0) continue;
+    int64_t plo = v.padded() ? v.plo[d] : 0;
+    e << " + (i64)(c" << d;
+    if (plo) e << " - " << plo;
+    e << ") * " << v.strides[d] << "ll";
+  }
+  e << ")";
+  return e.str();
+}
+
+// load leaf node ni for the current chunk: c_expr = coordinate of element j=0 along the vector axis
+void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
+  const RNode& n = node(ni);
+  const Leaf& l = R.leaves[n.leaf];
+  const View& v = l.view;
+  int vecaxis = flat ? rank - 1 : a;
+  std::string T = stype(l.dtype), C = ctype(l.dtype);
+  std::string P = "p" + std::to_string(slot_param.at(l.slot));
+  std::string base = "b" + std::to_string(n.leaf);
+  o << "      " << C << " f" << ni << "[" << V << "];\n";
+  if (leaf_vec[n.leaf]) {
+    o << "      { VecT<" << T << ", " << V << "> raw = *(const VecT<" << T << ", " << V << ">*)((const " << T << "*)" << P
+      << " + " << base << " + (" << ix() << ")(" << c_expr << "));\n";
+    o << "        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) f" << ni << "[j] = " << ld(l.dtype, "raw.v[j]")
+      << "; }\n";
+    return;
+  }
+  int64_t sa = v.strides[vecaxis];
+  o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) {\n";
+  std::string coord = "((i64)(" + c_expr + ") + j)";
+  std::string off = base + " + (" + ix() + ")(";
+  if (v.padded()) off += "(" + coord + " - " + std::to_string(v.plo[vecaxis]) + ")";
+  else off += coord;
+  off += " * " + std::to_string(sa) + "ll)";
+  std::string load = ld(l.dtype, "((const " + T + "*)" + P + ")[" + off + "]");
+  if (v.padded()) {
+    std::string inr = "(vb" + std::to_string(n.leaf) + " && " + coord + " >= " + std::to_string(v.plo[vecaxis]) +
+                      " && " + coord + " < " + std::to_string(v.plo[vecaxis] + (int64_t)v.src_shape[vecaxis]) + ")";
+    o << "        f" << ni << "[j] = " << inr << " ? " << load << " : (" << C << ")0;\n";
+  } else {
+    o << "        f" << ni << "[j] = " << load << ";\n";
+  }
+  o << "      }\n";
+}
+
+void Gen::emit_full_node(int ni, int phase, const std::string& c_expr) {
+  const RNode& n = node(ni);
+  bool from_cache = cached.count(ni) && first_phase[ni] < phase;
+  if (from_cache) {
+    o << "      " << ctype(n.dtype) << " (&f" << ni << ")[" << V << "] = cache" << ni << "[c];\n";
+    return;
+  }
+  if (n.kind == RK_LEAF) {
+    emit_leaf_load(ni, c_expr);
+  } else if (n.kind == (int)OpKind::Iota || n.kind == (int)OpKind::RandUniform) {
+    int vecaxis = flat ? rank - 1 : a;
+    o << "      " << ctype(n.dtype) << " f" << ni << "[" << V << "];\n";
+    o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) {\n";
+    if (n.kind == (int)OpKind::Iota) {
+      std::string coord = ((int)n.axis == vecaxis) ? "((i64)(" + c_expr + ") + j)" : "(i64)c" + std::to_string(n.axis);
+      o << "        f" << ni << "[j] = " << cast_expr(DType::I64, n.dtype, coord) << ";\n";
+    } else {
+      // flat index over S
+      std::vector<size_t> rs = row_major_strides(R.S);
+      std::ostringstream fi;
+      fi << "(u64)0";
+      for (int d = 0; d < rank; ++d) {
+        if (d == vecaxis) fi << " + ((u64)(" << c_expr << ") + (u64)j) * " << rs[d] << "ull";
+        else fi << " + (u64)c" << d << " * " << rs[d] << "ull";
+      }
+      o << "        f" << ni << "[j] = uniform_f32(threefry2x32((u64)(i64)" << val(n.in[0], "j") << ", " << fi.str()
+        << "));\n";
+    }
+    o << "      }\n";
+  } else {
+    o << "      " << ctype(n.dtype) << " f" << ni << "[" << V << "];\n";
+    o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) f" << ni << "[j] = " << op_expr(ni, "j")
+      << ";\n";
+  }
+  if (cached.count(ni) && first_phase[ni] == phase) {
+    o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) cache" << ni << "[c][j] = f" << ni
+      << "[j];\n";
+  }
+}
+
+void Gen::emit_line_node(int ni) {
+  const RNode& n = node(ni);
+  if (n.kind == RK_LEAF) {
+    const Leaf& l = R.leaves[n.leaf];
+    std::string P = "p" + std::to_string(slot_param.at(l.slot));
+    o << "  const " << ctype(n.dtype) << " s" << ni << " = " << ld(l.dtype, "((const " + std::string(stype(l.dtype)) + "*)" + P + ")[b" + std::to_string(n.leaf) + "]") << ";\n";
+  } else {
+    o << "  const " << ctype(n.dtype) << " s" << ni << " = " << op_expr(ni, "0") << ";\n";
+  }
+  auto it = out_slot.find(ni);
+  if (it != out_slot.end() && !full(ni) && !flat) {
+    o << "  if (lane == 0) ((" << stype(n.dtype) << "*)p" << slot_param.at(it->second) << ")[line] = "
+      << st(n.dtype, "s" + std::to_string(ni)) << ";\n";
+  }
+}
+
+void Gen::emit_red_init(int ni) {
+  const RNode& n = node(ni);
+  DType in = node(n.in[0]).dtype;
+  std::string r = std::to_string(ni);
+  if (n.kind == (int)OpKind::ArgReduce) {
+    bool mx = n.arg == ArgKind::Max;
+    std::string init;
+    if (fvalued(in) || in == DType::F64) init = flt_lit(in == DType::F64 ? DType::F64 : DType::F32, mx ? -INFINITY : INFINITY);
+    else init = mx ? int_min(in) : int_max(in);
+    o << "  " << ctype(in) << " bv" << r << " = " << init << "; i64 bi" << r << " = 9223372036854775807ll; bool bn" << r
+      << " = false;\n";
+    return;
+  }
+  DType acc = n.dtype;
+  std::string A;
+  if (fvalued(acc) || in == DType::F32) A = "float";
+  else if (acc == DType::F64) A = "double";
+  else A = n.kind == (int)OpKind::ReduceMax ? stype(acc) : utype(acc);
+  std::string init;
+  if (n.kind == (int)OpKind::Sum) init = "(" + A + ")0";
+  else if (n.kind == (int)OpKind::Prod) init = "(" + A + ")1";
+  else init = (A == "float" || A == "double") ? flt_lit(A == "double" ? DType::F64 : DType::F32, -INFINITY) : int_min(acc);
+  o << "  " << A << " acc" << r << " = " << init << ";\n";
+}
+
+void Gen::emit_red_update(int ni, const std::string& k_expr, const std::string& j) {
+  const RNode& n = node(ni);
+  DType in = node(n.in[0]).dtype;
+  std::string r = std::to_string(ni);
+  std::string v = val(n.in[0], j);
+  if (n.kind == (int)OpKind::ArgReduce) {
+    bool mx = n.arg == ArgKind::Max;
+    std::string cmp = mx ? ">" : "<";
+    std::string k = "((i64)(" + k_expr + "))";
+    if (fvalued(in) || in == DType::F64) {
+      o << "        { " << ctype(in) << " v_ = " << v << "; i64 k_ = " << k << "; if (k_ == 0 && v_ != v_) bn" << r
+        << " = true; if (v_ == v_ && (v_ " << cmp << " bv" << r << " || (v_ == bv" << r << " && k_ < bi" << r
+        << "))) { bv" << r << " = v_; bi" << r << " = k_; } }\n";
+    } else {
+      o << "        { " << ctype(in) << " v_ = " << v << "; i64 k_ = " << k << "; if (v_ " << cmp << " bv" << r
+        << " || (v_ == bv" << r << " && k_ < bi" << r << ")) { bv" << r << " = v_; bi" << r << " = k_; } }\n";
+    }
+    return;
+  }
+  bool fl = fvalued(n.dtype) || n.dtype == DType::F64 || in == DType::F32;
+  if (n.kind == (int)OpKind::Sum) {
+    if (fl) o << "        acc" << r << " += " << v << ";\n";
+    else o << "        acc" << r << " = acc" << r << " + (" << utype(n.dtype) << ")" << v << ";\n";
+  } else if (n.kind == (int)OpKind::Prod) {
+    if (fl) o << "        acc" << r << " *= " << v << ";\n";
+    else o << "        acc" << r << " = acc" << r << " * (" << utype(n.dtype) << ")" << v << ";\n";
+  } else {
+    if (n.dtype == DType::F64) o << "        acc" << r << " = fmax(acc" << r << ", " << v << ");\n";
+    else if (fl) o << "        acc" << r << " = fmaxf(acc" << r << ", " << v << ");\n";
+    else o << "        acc" << r << " = (" << v << " > acc" << r << ") ? " << v << " : acc" << r << ";\n";
+  }
+}
+
+// cross-lane fold of a reduction (butterfly within the wave, LDS across waves)
+void Gen::emit_red_finish(int ni, int phase) {
+  const RNode& n = node(ni);
+  std::string r = std::to_string(ni);
+  bool arg = n.kind == (int)OpKind::ArgReduce;
+  DType in = node(n.in[0]).dtype;
+  auto comb_arg = [&](const std::string& ov, const std::string& oi, const std::string& on) {
+    std::string cmp = n.arg == ArgKind::Max ? ">" : "<";
+    std::string ok = (fvalued(in) || in == DType::F64) ? "(" + ov + " == " + ov + ") && " : "";
+    return "{ if (" + ok + "(" + ov + " " + cmp + " bv" + r + " || (" + ov + " == bv" + r + " && " + oi + " < bi" + r +
+           "))) { bv" + r + " = " + ov + "; bi" + r + " = " + oi + "; } bn" + r + " = bn" + r + " || " + on + "; }";
+  };
+  auto comb = [&](const std::string& ov) {
+    if (n.kind == (int)OpKind::Sum) return "acc" + r + " = acc" + r + " + " + ov + ";";
+    if (n.kind == (int)OpKind::Prod) return "acc" + r + " = acc" + r + " * " + ov + ";";
+    if (n.dtype == DType::F64) return "acc" + r + " = fmax(acc" + r + ", " + ov + ");";
+    if (fvalued(n.dtype) || in == DType::F32) return "acc" + r + " = fmaxf(acc" + r + ", " + ov + ");";
+    return "acc" + r + " = (" + ov + " > acc" + r + ") ? " + ov + " : acc" + r + ";";
+  };
+  int wl = std::min(TPL, 64);
+  for (int m = wl / 2; m >= 1; m /= 2) {
+    if (arg)
+      o << "  { " << ctype(in) << " ov = shx(bv" << r << ", " << m << "); i64 oi = shx(bi" << r << ", " << m
+        << "); bool on = shx(bn" << r << ", " << m << "); " << comb_arg("ov", "oi", "on") << " }\n";
+    else
+      o << "  { auto ov = shx(acc" << r << ", " << m << "); " << comb("ov") << " }\n";
+  }
+  if (TPL > 64) {
+    int W = TPL / 64;
+    std::string tag = std::to_string(phase) + "_" + r;
+    if (arg) {
+      o << "  __shared__ " << ctype(in) << " lv" << tag << "[" << W << "]; __shared__ i64 li" << tag << "[" << W
+        << "]; __shared__ bool ln" << tag << "[" << W << "];\n";
+      o << "  if ((threadIdx.x & 63) == 0) { lv" << tag << "[threadIdx.x >> 6] = bv" << r << "; li" << tag
+        << "[threadIdx.x >> 6] = bi" << r << "; ln" << tag << "[threadIdx.x >> 6] = bn" << r << "; }\n";
+      o << "  __syncthreads();\n";
+      o << "  bv" << r << " = lv" << tag << "[0]; bi" << r << " = li" << tag << "[0]; bn" << r << " = ln" << tag << "[0];\n";
+      o << "  for (int w = 1; w < " << W << "; ++w) { " << ctype(in) << " ov = lv" << tag << "[w]; i64 oi = li" << tag
+        << "[w]; bool on = ln" << tag << "[w]; " << comb_arg("ov", "oi", "on") << " }\n";
+    } else {
+      o << "  __shared__ decltype(acc" << r << ") lr" << tag << "[" << W << "];\n";
+      o << "  if ((threadIdx.x & 63) == 0) lr" << tag << "[threadIdx.x >> 6] = acc" << r << ";\n";
+      o << "  __syncthreads();\n";
+      o << "  acc" << r << " = lr" << tag << "[0];\n";
+      o << "  for (int w = 1; w < " << W << "; ++w) { auto ov = lr" << tag << "[w]; " << comb("ov") << " }\n";
+    }
+  }
+  // final value
+  if (arg) {
+    o << "  const i64 s" << r << " = (bn" << r << " || bi" << r << " == 9223372036854775807ll) ? 0ll : bi" << r << ";\n";
+  } else {
+    std::string v = "acc" + r;
+    if (dt_is_int(n.dtype)) v = std::string("(") + stype(n.dtype) + ")" + v;
+    else v = rnd(n.dtype, v);
+    o << "  const " << ctype(n.dtype) << " s" << r << " = " << v << ";\n";
+  }
+  auto it = out_slot.find(ni);
+  if (it != out_slot.end()) {
+    o << "  if (lane == 0) ((" << stype(n.dtype) << "*)p" << slot_param.at(it->second) << ")[line] = "
+      << st(n.dtype, "s" + r) << ";\n";
+  }
+}
+
+std::string Gen::generate(RegionCode* rc) {
+  plan_layout();
+  schedule();
+  std::ostringstream nm;
+  nm << "ku_" << (flat ? "ew" : "line") << index;
+  std::string entry = nm.str();
+  for (auto& l : R.leaves) param(l.slot);
+  for (auto& op : R.outputs) param(op.second);
+  o << kDevicePrelude;
+  o << "extern \"C\" __global__ void __launch_bounds__(" << WG << ") " << entry << "(";
+  for (size_t i = 0; i < param_slots.size(); ++i) o << (i ? ", " : "") << "void* __restrict__ p" << i;
+  o << ") {\n";
+  int vecaxis = flat ? rank - 1 : a;
+  std::vector<int> lines_leaves;
+  if (flat) {
+    uint64_t chunks = N / V;
+    o << "  const u64 chunk = (u64)blockIdx.x * " << WG << "ull + threadIdx.x;\n";
+    o << "  if (chunk >= " << chunks << "ull) return;\n";
+    o << "  const int lane = 0; (void)lane;\n";
+    o << "  " << ix() << " t = (" << ix() << ")(chunk * " << V << "ull);\n";
+    for (int d = rank - 1; d >= 0; --d) {
+      o << "  const " << ix() << " c" << d << " = t % " << R.S[d] << "u; t /= " << R.S[d] << "u;\n";
+    }
+    o << "  (void)t;\n";
+  } else {
+    o << "  const u32 lane = threadIdx.x % " << TPL << "u;\n";
+    o << "  const u64 line = (u64)blockIdx.x * " << GPW << "ull + threadIdx.x / " << TPL << "u;\n";
+    if ((uint64_t)GPW * (((lines + GPW - 1) / GPW)) != lines) o << "  if (line >= " << lines << "ull) return;\n";
+    o << "  " << ix() << " t = (" << ix() << ")line;\n";
+    for (int d = rank - 1; d >= 0; --d) {
+      if (d == a) continue;
+      o << "  const " << ix() << " c" << d << " = t % " << R.S[d] << "u; t /= " << R.S[d] << "u;\n";
+    }
+    o << "  (void)t;\n";
+  }
+  // leaf bases (+ padding validity on the non-vector axes)
+  for (size_t li = 0; li < R.leaves.size(); ++li) {
+    o << "  const " << ix() << " b" << li << " = " << leaf_base((int)li) << ";\n";
+    const View& v = R.leaves[li].view;
+    if (v.padded()) {
+      o << "  const bool vb" << li << " = true";
+      for (int d = 0; d < rank; ++d) {
+        if (d == vecaxis) continue;
+        o << " && (i64)c" << d << " >= " << v.plo[d] << " && (i64)c" << d << " < " << v.plo[d] + (int64_t)v.src_shape[d];
+      }
+      o << ";\n";
+    }
+  }
+  if (flat) {
+    // single pass over V elements
+    std::string cexpr = "c" + std::to_string(rank - 1);
+    std::set<int> needed;
+    std::function<void(int)> add = [&](int n) {
+      if (needed.count(n)) return;
+      needed.insert(n);
+      for (int i : node(n).in) add(i);
+    };
+    for (auto& op : R.outputs) add(op.first);
+    o << "  {\n";
+    for (size_t i = 0; i < R.nodes.size(); ++i)
+      if (needed.count((int)i)) emit_full_node((int)i, 1, cexpr);
+    for (auto& op : R.outputs) {
+      const RNode& n = node(op.first);
+      std::string T = stype(n.dtype);
+      std::string P = "p" + std::to_string(slot_param.at(op.second));
+      if (V > 1) {
+        o << "    { VecT<" << T << ", " << V << "> w;\n      #pragma unroll\n      for (int j = 0; j < " << V
+          << "; ++j) w.v[j] = " << st(n.dtype, "f" + std::to_string(op.first) + "[j]") << ";\n      *(VecT<" << T << ", "
+          << V << ">*)((" << T << "*)" << P << " + chunk * " << V << "ull) = w; }\n";
+      } else {
+        o << "    ((" << T << "*)" << P << ")[chunk] = " << st(n.dtype, "f" + std::to_string(op.first) + "[0]") << ";\n";
+      }
+    }
+    o << "  }\n}\n";
+    rc->grid = (unsigned)((N / (uint64_t)V + WG - 1) / WG);
+    rc->block = WG;
+    rc->entry = entry;
+    rc->arg_slots = param_slots;
+    return o.str();
+  }
+  // ---- line kernel ----
+  // caches
+  for (int c : cached) o << "  " << ctype(node(c).dtype) << " cache" << c << "[" << NC << "][" << V << "];\n";
+  // line-level (level 0) LINE nodes
+  for (size_t i = 0; i < R.nodes.size(); ++i)
+    if (!full((int)i) && node((int)i).level == 0 && !is_red(node((int)i).kind)) emit_line_node((int)i);
+  std::vector<size_t> rs = row_major_strides(R.S);
+  int nph = P + (has_final ? 1 : 0);
+  for (int p = 1; p <= nph; ++p) {
+    std::vector<int> reds;
+    for (size_t i = 0; i < R.nodes.size(); ++i)
+      if (is_red(node((int)i).kind) && node((int)i).level == p) reds.push_back((int)i);
+    for (int r : reds) emit_red_init(r);
+    // chunk loop
+    if (unroll) o << "  #pragma unroll\n";
+    else o << "  #pragma unroll 2\n";
+    o << "  for (int c = 0; c < " << NC << "; ++c) {\n";
+    o << "    const u32 ch = (u32)c * " << TPL << "u + lane;\n";
+    bool guard = (uint64_t)NC * TPL * V != L;
+    if (guard) o << "    if ((u64)ch * " << V << "ull < " << L << "ull) {\n";
+    else o << "    {\n";
+    std::string cexpr = "ch * " + std::to_string(V) + "u";
+    for (size_t i = 0; i < R.nodes.size(); ++i)
+      if (need[p].count((int)i)) emit_full_node((int)i, p, cexpr);
+    for (int r : reds) {
+      o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) {\n";
+      emit_red_update(r, "ch * " + std::to_string(V) + "u + j", "j");
+      o << "      }\n";
+    }
+    // FULL outputs stored in this phase
+    for (auto& op : R.outputs) {
+      if (!full(op.first) || store_phase[op.first] != p) continue;
+      const RNode& n = node(op.first);
+      std::string T = stype(n.dtype);
+      std::string Pp = "p" + std::to_string(slot_param.at(op.second));
+      // output offset: row-major over S
+      std::ostringstream ob;
+      ob << "(" << ix() << ")(0";
+      for (int d = 0; d < rank; ++d)
+        if (d != a) ob << " + (" << ix() << ")c" << d << " * " << rs[d] << "u";
+      ob << ")";
+      if (V > 1 && rs[a] == 1) {
+        o << "      { VecT<" << T << ", " << V << "> w;\n        #pragma unroll\n        for (int j = 0; j < " << V
+          << "; ++j) w.v[j] = " << st(n.dtype, val(op.first, "j")) << ";\n        *(VecT<" << T << ", " << V << ">*)(("
+          << T << "*)" << Pp << " + " << ob.str() << " + (" << ix() << ")(" << cexpr << ")) = w; }\n";
+      } else {
+        o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) ((" << T << "*)" << Pp << ")["
+          << ob.str() << " + ((" << ix() << ")(" << cexpr << ") + j) * " << rs[a] << "u] = "
+          << st(n.dtype, val(op.first, "j")) << ";\n";
+      }
+    }
+    o << "    }\n  }\n";
+    for (int r : reds) emit_red_finish(r, p);
+    for (size_t i = 0; i < R.nodes.size(); ++i)
+      if (!full((int)i) && node((int)i).level == p && !is_red(node((int)i).kind)) emit_line_node((int)i);
+  }
+  o << "}\n";
+  rc->grid = (unsigned)((lines + GPW - 1) / GPW);
+  rc->block = WG;
+  rc->entry = entry;
+  rc->arg_slots = param_slots;
+  return o.str();
+}
+
+}  // namespace
+
+RegionCode gen_region(const Region& r, const std::vector<Slot>& slots, int index) {
+  Gen g(r, slots, index);
+  RegionCode rc;
+  rc.src = g.generate(&rc);
+  return rc;
+}
+
+}  // namespace ku::hipbk

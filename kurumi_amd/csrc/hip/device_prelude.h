@@ -1,0 +1,115 @@
+// Device-side helpers prepended to every generated region kernel (compiled by hipRTC
+// for gfx950). Conversions follow the reference's cast semantics
+// (kurumi_core/src/dtype/convert.rs:14-70, dtype/traits/elem.rs:31-45): round to nearest
+// even, f64 sources rounded once (round-to-odd intermediate), e4m3 saturating to +-448,
+// float -> int truncating and saturating with NaN -> 0. threefry2x32-20 is the reference
+// RNG (kurumi_core/src/rng.rs:10-31).
+#pragma once
+
+namespace ku::hipbk {
+
+inline const char* kDevicePrelude = R"KUPRELUDE(
+#ifndef INFINITY
+#define INFINITY __builtin_inff()
+#endif
+typedef unsigned char u8; typedef unsigned short u16; typedef unsigned int u32; typedef unsigned long long u64;
+typedef signed char i8; typedef short i16; typedef int i32; typedef long long i64;
+template <class T, int N> struct __attribute__((aligned(sizeof(T) * N))) VecT { T v[N]; };
+#define KD __device__ __forceinline__
+KD float bf16_ld(u16 h) { return __uint_as_float(((u32)h) << 16); }
+KD u16 bf16_st(float f) {
+  u32 u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (u16)(u >> 16);
+}
+KD float rbf16(float f) { return bf16_ld(bf16_st(f)); }
+KD float f16_ld(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
+KD u16 f16_st(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
+KD float rf16(float f) { return (float)(_Float16)f; }
+// f64 -> f32 rounded to odd: a later RNE to a narrower format then rounds exactly once
+KD float f32_odd(double x) {
+  float f = (float)x;
+  if ((double)f != x && !(__float_as_uint(f) & 1u)) f = nextafterf(f, (double)f < x ? INFINITY : -INFINITY);
+  return f;
+}
+KD float rbf16_d(double x) { return rbf16(f32_odd(x)); }
+KD float rf16_d(double x) { return rf16(f32_odd(x)); }
+KD float f8e4m3_ld(u8 b) {
+  u32 e = (b >> 3) & 15u, m = b & 7u;
+  float v;
+  if (e == 15u && m == 7u) v = __uint_as_float(0x7fc00000u);
+  else if (e == 0u) v = (float)m * 0.001953125f;
+  else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
+  return (b & 0x80u) ? -v : v;
+}
+KD u8 f8e4m3_st(float x) {
+  u32 u = __float_as_uint(x);
+  u32 s = (u >> 24) & 0x80u;
+  if (x != x) return (u8)(s | 0x7fu);
+  float a = fabsf(x);
+  if (a > 448.f) return (u8)(s | 0x7eu);
+  if (a < 0.015625f) return (u8)(s | (u32)rintf(a * 512.f));
+  int E = (int)((u >> 23) & 0xffu) - 127;
+  float q = __uint_as_float((u32)(E - 3 + 127) << 23);
+  u32 n = (u32)rintf(a / q);
+  u32 r = ((u32)(E + 7) << 3) + (n - 8u);
+  if (r > 0x7eu) r = 0x7eu;
+  return (u8)(s | r);
+}
+KD float rf8e4m3(float x) { return f8e4m3_ld(f8e4m3_st(x)); }
+KD float f8e5m2_ld(u8 b) {
+  u32 e = (b >> 2) & 31u, m = b & 3u;
+  float v;
+  if (e == 31u) v = m ? __uint_as_float(0x7fc00000u) : INFINITY;
+  else if (e == 0u) v = (float)m * 1.52587890625e-05f;
+  else v = __uint_as_float(((e + 112u) << 23) | (m << 21));
+  return (b & 0x80u) ? -v : v;
+}
+KD u8 f8e5m2_st(float x) {
+  u32 u = __float_as_uint(x);
+  u32 s = (u >> 24) & 0x80u;
+  if (x != x) return (u8)(s | 0x7eu);
+  float a = fabsf(x);
+  if (a >= 61440.f) return (u8)(s | 0x7cu);
+  if (a < 6.103515625e-05f) return (u8)(s | (u32)rintf(a * 65536.f));
+  int E = (int)((u >> 23) & 0xffu) - 127;
+  float q = __uint_as_float((u32)(E - 2 + 127) << 23);
+  u32 n = (u32)rintf(a / q);
+  return (u8)(s | (((u32)(E + 15) << 2) + (n - 4u)));
+}
+KD float rf8e5m2(float x) { return f8e5m2_ld(f8e5m2_st(x)); }
+template <class I> KD I sat_int(double x);
+#define KU_SAT(I, LO, HI) template <> KD I sat_int<I>(double x) { \
+  if (x != x) return (I)0; if (x <= (double)(LO)) return (I)(LO); if (x >= (double)(HI)) return (I)(HI); return (I)x; }
+KU_SAT(u8, 0, 255) KU_SAT(u16, 0, 65535) KU_SAT(u32, 0u, 4294967295u) KU_SAT(u64, 0ull, 18446744073709551615ull)
+KU_SAT(i8, -128, 127) KU_SAT(i16, -32768, 32767) KU_SAT(i32, -2147483648ll, 2147483647ll)
+KU_SAT(i64, (-9223372036854775807ll - 1), 9223372036854775807ll)
+KD u32 rotl32(u32 x, u32 r) { return (x << r) | (x >> (32u - r)); }
+KD u64 threefry2x32(u64 key, u64 ctr) {
+  const u32 k0 = (u32)key, k1 = (u32)(key >> 32), k2 = 0x1BD11BDAu ^ k0 ^ k1;
+  u32 x0 = (u32)ctr + k0, x1 = (u32)(ctr >> 32) + k1;
+#define KU_TF(R) x0 += x1; x1 = rotl32(x1, R); x1 ^= x0;
+#define KU_INJ(A, B, I) x0 += A; x1 += B + I;
+  KU_TF(13) KU_TF(15) KU_TF(26) KU_TF(6) KU_INJ(k1, k2, 1u)
+  KU_TF(17) KU_TF(29) KU_TF(16) KU_TF(24) KU_INJ(k2, k0, 2u)
+  KU_TF(13) KU_TF(15) KU_TF(26) KU_TF(6) KU_INJ(k0, k1, 3u)
+  KU_TF(17) KU_TF(29) KU_TF(16) KU_TF(24) KU_INJ(k1, k2, 4u)
+  KU_TF(13) KU_TF(15) KU_TF(26) KU_TF(6) KU_INJ(k2, k0, 5u)
+  return (u64)x0 | ((u64)x1 << 32);
+}
+KD float uniform_f32(u64 bits) { return (float)((u32)bits >> 8) / 16777216.f; }
+KD float shx(float v, int m) { return __shfl_xor(v, m, 64); }
+KD double shx(double v, int m) { return __shfl_xor(v, m, 64); }
+KD i32 shx(i32 v, int m) { return __shfl_xor(v, m, 64); }
+KD u32 shx(u32 v, int m) { return __shfl_xor((i32)v, m, 64); }
+KD i64 shx(i64 v, int m) { return __shfl_xor((long long)v, m, 64); }
+KD u64 shx(u64 v, int m) { return (u64)__shfl_xor((long long)v, m, 64); }
+KD i8 shx(i8 v, int m) { return (i8)__shfl_xor((i32)v, m, 64); }
+KD u8 shx(u8 v, int m) { return (u8)__shfl_xor((i32)v, m, 64); }
+KD i16 shx(i16 v, int m) { return (i16)__shfl_xor((i32)v, m, 64); }
+KD u16 shx(u16 v, int m) { return (u16)__shfl_xor((i32)v, m, 64); }
+KD bool shx(bool v, int m) { return __shfl_xor((i32)v, m, 64) != 0; }
+)KUPRELUDE";
+
+}  // namespace ku::hipbk

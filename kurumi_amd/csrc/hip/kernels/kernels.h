@@ -1,0 +1,46 @@
+// Host-side launchers of the precompiled gfx950 kernels (GEMM and flash attention).
+// Fused pointwise/reduce kernels are generated at run time (codegen.cpp) instead.
+#pragma once
+#include <hip/hip_runtime_api.h>
+
+#include <cstdint>
+
+namespace ku::hipbk {
+
+// Element type tags for the GEMM launchers (match ku::DType values).
+enum GemmType : int { GT_F8E4M3 = 9, GT_F8E5M2 = 10, GT_F16 = 11, GT_BF16 = 12, GT_F32 = 13, GT_F64 = 14, GT_I32 = 7, GT_I64 = 8 };
+
+struct GemmArgs {
+  const void* a = nullptr;
+  const void* b = nullptr;
+  void* c = nullptr;
+  int64_t sab = 0, sam = 0, sak = 0;  // A[b][m][k] element strides
+  int64_t sbb = 0, sbk = 0, sbn = 0;  // B[b][k][n] element strides
+  int64_t batch = 1, m = 0, n = 0, k = 0;
+  int in_type = GT_BF16;
+  int out_type = GT_BF16;
+  // optional epilogue: c = acc * alpha[0] * col_scale[n * col_scale_stride]
+  const float* alpha = nullptr;
+  const float* col_scale = nullptr;
+  int64_t col_scale_stride = 1;
+};
+
+// Returns a short name of the kernel variant that will run (for plan labels).
+const char* gemm_variant(const GemmArgs& a);
+void launch_gemm(const GemmArgs& a, hipStream_t s);
+
+struct AttnArgs {
+  const void* q = nullptr;
+  const void* k = nullptr;
+  const void* v = nullptr;
+  void* o = nullptr;
+  int64_t bh = 0, s = 0, d = 0;  // [bh, s, d] contiguous
+  float scale = 1.f;
+  bool causal = false;
+  int dtype = GT_BF16;
+};
+const char* attn_variant(const AttnArgs& a);
+bool attn_supported(const AttnArgs& a);
+void launch_attention(const AttnArgs& a, hipStream_t s);
+
+}  // namespace ku::hipbk

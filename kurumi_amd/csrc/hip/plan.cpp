@@ -1,0 +1,1420 @@
+// Fusion planner + plan executor for the HIP backend (see plan.h).
+#include "plan.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <functional>
+#include <limits>
+#include <sstream>
+#include <unordered_map>
+
+#include "kernels/kernels.h"
+
+namespace ku::hipbk {
+
+// ======================= views =======================
+
+View View::contiguous(const Shape& s) {
+  View v;
+  v.shape = s;
+  auto st = row_major_strides(s);
+  v.strides.assign(st.begin(), st.end());
+  return v;
+}
+
+bool View::is_contiguous() const {
+  if (padded() || offset != 0) return false;
+  auto st = row_major_strides(shape);
+  for (size_t i = 0; i < shape.size(); ++i)
+    if (shape[i] != 1 && strides[i] != (int64_t)st[i]) return false;
+  return true;
+}
+
+// No-copy reshape (dims grouped by equal products; each old group must be dense).
+bool view_reshape(const View& v, const Shape& to, View* out) {
+  if (v.padded()) return false;
+  if (numel(v.shape) == 0) {
+    *out = View::contiguous(to);
+    out->offset = v.offset;
+    return true;
+  }
+  std::vector<size_t> os;
+  std::vector<int64_t> ost;
+  for (size_t i = 0; i < v.shape.size(); ++i)
+    if (v.shape[i] != 1) os.push_back(v.shape[i]), ost.push_back(v.strides[i]);
+  View r;
+  r.shape = to;
+  r.strides.assign(to.size(), 0);
+  r.offset = v.offset;
+  size_t oi = 0, ni = 0;
+  while (ni < to.size() || oi < os.size()) {
+    if (ni < to.size() && to[ni] == 1) { r.strides[ni] = 0; ++ni; continue; }
+    if (ni >= to.size() || oi >= os.size()) return false;
+    size_t o0 = oi, n0 = ni;
+    size_t po = os[oi++], pn = to[ni++];
+    while (po != pn) {
+      if (po < pn) {
+        if (oi >= os.size()) return false;
+        po *= os[oi++];
+      } else {
+        while (ni < to.size() && to[ni] == 1) r.strides[ni++] = 0;
+        if (ni >= to.size()) return false;
+        pn *= to[ni++];
+      }
+    }
+    for (size_t t = o0; t + 1 < oi; ++t)
+      if (ost[t] != ost[t + 1] * (int64_t)os[t + 1]) return false;
+    int64_t stride = ost[oi - 1];
+    for (size_t t = ni; t-- > n0;) {
+      if (to[t] == 1) { r.strides[t] = 0; continue; }
+      r.strides[t] = stride;
+      stride *= (int64_t)to[t];
+    }
+  }
+  *out = r;
+  return true;
+}
+
+View view_expand(const View& v, const Shape& to) {
+  View r = v;
+  r.shape = to;
+  for (size_t i = 0; i < to.size(); ++i)
+    if (v.shape[i] == 1 && to[i] != 1) r.strides[i] = 0;
+  return r;
+}
+
+View view_permute(const View& v, const std::vector<size_t>& perm) {
+  View r;
+  r.offset = v.offset;
+  for (size_t p : perm) {
+    r.shape.push_back(v.shape[p]);
+    r.strides.push_back(v.strides[p]);
+  }
+  return r;
+}
+
+View view_slice(const View& v, const std::vector<SliceRange>& rg) {
+  View r = v;
+  for (size_t i = 0; i < rg.size(); ++i) {
+    r.offset += (int64_t)rg[i].start * v.strides[i];
+    r.strides[i] = v.strides[i] * (int64_t)rg[i].step;
+    r.shape[i] = (rg[i].end - rg[i].start + rg[i].step - 1) / rg[i].step;
+  }
+  return r;
+}
+
+View view_flip(const View& v, const std::vector<size_t>& axes) {
+  View r = v;
+  for (size_t a : axes) {
+    if (r.shape[a] == 0) continue;
+    r.offset += (int64_t)(r.shape[a] - 1) * r.strides[a];
+    r.strides[a] = -r.strides[a];
+  }
+  return r;
+}
+
+View view_pad(const View& v, const std::vector<PadRange>& p) {
+  View r = v;
+  r.src_shape = v.shape;
+  r.plo.resize(p.size());
+  for (size_t i = 0; i < p.size(); ++i) {
+    r.plo[i] = (int64_t)p[i].lo;
+    r.shape[i] = p[i].lo + v.shape[i] + p[i].hi;
+  }
+  return r;
+}
+
+static bool view_eq(const View& a, const View& b) {
+  return a.shape == b.shape && a.strides == b.strides && a.offset == b.offset && a.plo == b.plo &&
+         a.src_shape == b.src_shape;
+}
+
+// ======================= const cache =======================
+
+DevBuf ConstCache::get(const Graph& g, NodeId id) {
+  auto key = std::make_pair(g.id(), id);
+  auto it = map_.find(key);
+  if (it != map_.end()) return it->second;
+  const Node& n = g.node(id);
+  DevBuf b = ctx_->pool().alloc(std::max<size_t>(n.op.data->size(), 1));
+  if (!n.op.data->empty())
+    KU_HIP(hipMemcpyAsync(b.ptr, n.op.data->data(), n.op.data->size(), hipMemcpyHostToDevice, ctx_->stream()));
+  map_[key] = b;
+  return b;
+}
+
+void ConstCache::drop_graph(uint64_t gid) {
+  for (auto it = map_.begin(); it != map_.end();) {
+    if (it->first.first == gid) {
+      ctx_->pool().release(it->second);
+      it = map_.erase(it);
+    } else {
+      ++it;
+    }
+  }
+}
+
+ConstCache::~ConstCache() {
+  for (auto& kv : map_) ctx_->pool().release(kv.second);
+}
+
+// ======================= planner =======================
+
+namespace {
+
+constexpr size_t kEmpty = std::numeric_limits<size_t>::max();
+
+struct Val {
+  enum K { None, Dev, LFull, LLine, LKeep, LBcast } k = None;
+  int slot = -1;
+  View view;
+  int region = -1;
+  int rn = -1;
+};
+
+bool is_elementwise(OpKind k) {
+  switch (k) {
+    case OpKind::Cast: case OpKind::Bitcast: case OpKind::Add: case OpKind::Mul: case OpKind::Max:
+    case OpKind::Neg: case OpKind::IDiv: case OpKind::And: case OpKind::Or: case OpKind::Xor: case OpKind::Shl:
+    case OpKind::Shr: case OpKind::CmpLt: case OpKind::CmpEq: case OpKind::Where: case OpKind::Recip:
+    case OpKind::Sqrt: case OpKind::Exp2: case OpKind::Log2: case OpKind::Sin: case OpKind::Floor:
+      return true;
+    default:
+      return false;
+  }
+}
+bool is_reduce(OpKind k) {
+  return k == OpKind::Sum || k == OpKind::Prod || k == OpKind::ReduceMax || k == OpKind::ArgReduce;
+}
+
+Shape drop_axis(const Shape& s, int a) {
+  Shape r = s;
+  r.erase(r.begin() + a);
+  return r;
+}
+Shape keep_axis(const Shape& s, int a) {
+  Shape r = s;
+  r[a] = 1;
+  return r;
+}
+
+// value of a scalar constant (all elements equal) or NaN when not uniform
+bool const_uniform_value(const Node& n, double* out) {
+  if (n.op.kind != OpKind::Const || !n.op.data) return false;
+  size_t cnt = numel(n.op.shape);
+  if (cnt == 0) return false;
+  size_t w = dt_width(n.op.data_dtype);
+  const uint8_t* p = n.op.data->data();
+  for (size_t i = 1; i < cnt; ++i)
+    if (std::memcmp(p, p + i * w, w) != 0) return false;
+  double v;
+  switch (n.op.data_dtype) {
+    case DType::F32: { float f; std::memcpy(&f, p, 4); v = f; } break;
+    case DType::F64: std::memcpy(&v, p, 8); break;
+    case DType::BF16: { uint16_t h; std::memcpy(&h, p, 2); v = bf16_to_f32(h); } break;
+    case DType::F16: { uint16_t h; std::memcpy(&h, p, 2); v = f16_to_f64(h); } break;
+    default: return false;
+  }
+  *out = v;
+  return true;
+}
+
+}  // namespace
+
+class Planner {
+ public:
+  Planner(Plan& P, ConstCache* consts) : P_(P), g_(P.g_), consts_(consts) {}
+  void run();
+
+ private:
+  // slots / steps
+  int new_slot(SlotKind k, DType dt, size_t bytes, NodeId node) {
+    Slot s;
+    s.kind = k;
+    s.dtype = dt;
+    s.bytes = bytes;
+    s.node = node;
+    P_.slots_.push_back(s);
+    slot_producer_.push_back(-1);
+    return (int)P_.slots_.size() - 1;
+  }
+  int new_step(Step::Type t, int index, const std::string& label) {
+    Step s;
+    s.type = t;
+    s.index = index;
+    s.label = label;
+    P_.steps_.push_back(s);
+    step_alive_.push_back(true);
+    return (int)P_.steps_.size() - 1;
+  }
+  int new_region(const Shape& S) {
+    Region r;
+    r.S = S;
+    if (r.S.empty()) r.S = {1};
+    P_.regions_.push_back(r);
+    int id = (int)P_.regions_.size() - 1;
+    region_step_.push_back(new_step(Step::REGION, id, "fused"));
+    return id;
+  }
+  void depend(int step, int slot) {
+    int p = slot_producer_[slot];
+    if (p >= 0 && p != step) P_.steps_[step].deps.insert(p);
+  }
+
+  // region building
+  int add_leaf(int rid, int slot, const View& v, DType dt);
+  int add_node(int rid, RNode n);
+  void set_level(Region& R, RNode& n);
+  void materialize(NodeId x);
+  int output_slot(int rid, int rn);
+  View dev_view_of(NodeId x);
+  int region_operand(int rid, NodeId x, bool line_pos);
+  bool try_join(NodeId id, int* rid_out, bool* line_pos);
+  void merge_regions(int into, int from);
+  void close_region(int rid) { P_.regions_[rid].closed = true; }
+
+  void visit(NodeId id);
+  void visit_elementwise(NodeId id);
+  void visit_movement(NodeId id);
+  void visit_reduce(NodeId id);
+  void visit_rowop(NodeId id);
+  void visit_dot(NodeId id);
+  void visit_sdpa(NodeId id);
+  int copy_view_to_slot(const View& v, int slot_src, DType dt, NodeId node);
+
+  // pattern pre-pass
+  void find_patterns();
+  bool match_attention(NodeId d2);
+  bool match_fp8_epilogue(NodeId castn);
+
+  struct AttnPattern { NodeId q, k, v; float scale; bool causal; };
+  struct Fp8Pattern { NodeId dot, xq, wq, sx, sw; };
+
+  Plan& P_;
+  const Graph& g_;
+  ConstCache* consts_;
+  std::vector<Val> vals_;
+  std::vector<int> consumers_;
+  std::vector<bool> absorbed_;
+  std::map<NodeId, AttnPattern> attn_pat_;
+  std::map<NodeId, Fp8Pattern> fp8_pat_;
+  std::vector<int> region_step_;
+  std::vector<int> slot_producer_;
+  std::vector<bool> step_alive_;
+  std::map<std::pair<int, int>, int> rn_slot_;
+  std::set<NodeId> root_set_;
+};
+
+int Planner::add_leaf(int rid, int slot, const View& v, DType dt) {
+  Region& R = P_.regions_[rid];
+  for (size_t i = 0; i < R.leaves.size(); ++i)
+    if (R.leaves[i].slot == slot && R.leaves[i].dtype == dt && view_eq(R.leaves[i].view, v)) {
+      for (size_t j = 0; j < R.nodes.size(); ++j)
+        if (R.nodes[j].kind == RK_LEAF && R.nodes[j].leaf == (int)i) return (int)j;
+    }
+  Leaf L;
+  L.slot = slot;
+  L.view = v;
+  L.dtype = dt;
+  R.leaves.push_back(L);
+  depend(region_step_[rid], slot);
+  RNode n;
+  n.kind = RK_LEAF;
+  n.leaf = (int)R.leaves.size() - 1;
+  n.dtype = dt;
+  // a leaf that is constant along the axis is a LINE value
+  n.space = (R.axis >= 0 && v.strides[R.axis] == 0 && !v.padded()) ? Space::Line : Space::Full;
+  if (R.axis < 0) n.space = Space::Full;
+  return add_node(rid, n);
+}
+
+void Planner::set_level(Region& R, RNode& n) {
+  int lv = 0;
+  for (int i : n.in) lv = std::max(lv, R.nodes[i].level);
+  if (is_reduce((OpKind)n.kind)) lv += 1;
+  n.level = lv;
+}
+
+int Planner::add_node(int rid, RNode n) {
+  Region& R = P_.regions_[rid];
+  set_level(R, n);
+  R.nodes.push_back(n);
+  return (int)R.nodes.size() - 1;
+}
+
+int Planner::output_slot(int rid, int rn) {
+  auto key = std::make_pair(rid, rn);
+  auto it = rn_slot_.find(key);
+  if (it != rn_slot_.end()) return it->second;
+  Region& R = P_.regions_[rid];
+  const RNode& n = R.nodes[rn];
+  Shape sh = n.space == Space::Full ? R.S : drop_axis(R.S, R.axis);
+  int slot = new_slot(SlotKind::Temp, n.dtype, numel(sh) * dt_width(n.dtype), 0);
+  slot_producer_[slot] = region_step_[rid];
+  R.outputs.push_back({rn, slot});
+  rn_slot_[key] = slot;
+  return slot;
+}
+
+// Turn a lazy value into a device buffer (its region gains an output and is closed:
+// whatever reads the buffer runs after the region's kernel).
+void Planner::materialize(NodeId x) {
+  Val& v = vals_[x];
+  if (v.k == Val::Dev) return;
+  if (v.k == Val::None) throw Error("kurumi_hip planner: node " + std::to_string(x) + " has no value");
+  int rid = v.region;
+  Region& R = P_.regions_[rid];
+  int slot = output_slot(rid, v.rn);
+  close_region(rid);
+  const Shape& gs = g_.shape(x);
+  View view;
+  if (v.k == Val::LFull) {
+    view = View::contiguous(R.S);
+    if (!view_reshape(view, gs, &view)) throw Error("planner: bad full view");
+  } else if (v.k == Val::LLine || v.k == Val::LKeep) {
+    view = View::contiguous(drop_axis(R.S, R.axis));
+    if (!view_reshape(view, gs, &view)) throw Error("planner: bad line view");
+  } else {  // LBcast: the line buffer broadcast along the axis
+    View lk = View::contiguous(drop_axis(R.S, R.axis));
+    View kd;
+    if (!view_reshape(lk, keep_axis(R.S, R.axis), &kd)) throw Error("planner: bad keepdim view");
+    view = view_expand(kd, R.S);
+    if (gs != R.S && !view_reshape(view, gs, &view)) throw Error("planner: bad bcast view");
+  }
+  // every graph node sharing this lazy value becomes the same device view
+  for (size_t i = 0; i < vals_.size(); ++i) {
+    Val& o = vals_[i];
+    if (o.k != Val::Dev && o.k != Val::None && o.region == rid && o.rn == v.rn && o.k == v.k &&
+        g_.shape((NodeId)i) == gs) {
+      o.k = Val::Dev;
+      o.slot = slot;
+      o.view = view;
+    }
+  }
+}
+
+View Planner::dev_view_of(NodeId x) {
+  materialize(x);
+  return vals_[x].view;
+}
+
+// Operand of a region node: a lazy member or a device leaf viewed over R.S.
+int Planner::region_operand(int rid, NodeId x, bool line_pos) {
+  Val& v = vals_[x];
+  Region& R = P_.regions_[rid];
+  if (v.k != Val::Dev) return v.rn;  // caller checked compatibility
+  View view = v.view;
+  if (line_pos) {
+    // x has the line shape (S without the axis): insert a stride-0 axis
+    View kd;
+    if (!view_reshape(view, keep_axis(R.S, R.axis), &kd)) {
+      // not representable (padded view): copy first
+      int s = copy_view_to_slot(view, v.slot, g_.dtype(x), x);
+      View c = View::contiguous(g_.shape(x));
+      view_reshape(c, keep_axis(R.S, R.axis), &kd);
+      v.slot = s;
+      v.view = c;
+    }
+    view = view_expand(kd, R.S);
+  } else if (g_.shape(x) != R.S) {
+    View r;
+    if (!view_reshape(view, R.S, &r)) throw Error("planner: operand shape mismatch");
+    view = r;
+  }
+  return add_leaf(rid, v.slot, view, g_.dtype(x));
+}
+
+void Planner::merge_regions(int into, int from) {
+  Region& A = P_.regions_[into];
+  Region& B = P_.regions_[from];
+  if (A.axis < 0) A.axis = B.axis;
+  int base = (int)A.nodes.size();
+  int lbase = (int)A.leaves.size();
+  for (auto& L : B.leaves) A.leaves.push_back(L);
+  for (RNode n : B.nodes) {
+    for (int& i : n.in) i += base;
+    if (n.kind == RK_LEAF) n.leaf += lbase;
+    A.nodes.push_back(n);
+  }
+  for (auto& o : B.outputs) {
+    A.outputs.push_back({o.first + base, o.second});
+    slot_producer_[o.second] = region_step_[into];
+  }
+  for (auto it = rn_slot_.begin(); it != rn_slot_.end();) {
+    if (it->first.first == from) {
+      rn_slot_[{into, it->first.second + base}] = it->second;
+      it = rn_slot_.erase(it);
+    } else {
+      ++it;
+    }
+  }
+  for (auto& v : vals_)
+    if (v.k != Val::Dev && v.k != Val::None && v.region == from) {
+      v.region = into;
+      v.rn += base;
+    }
+  Step& sa = P_.steps_[region_step_[into]];
+  for (int d : P_.steps_[region_step_[from]].deps) sa.deps.insert(d);
+  step_alive_[region_step_[from]] = false;
+  B.nodes.clear();
+  B.leaves.clear();
+  B.outputs.clear();
+  B.closed = true;
+  // re-derive leaf spaces for the (possibly new) axis
+  for (auto& n : A.nodes)
+    if (n.kind == RK_LEAF && A.axis >= 0) {
+      const View& lv = A.leaves[n.leaf].view;
+      n.space = (lv.strides[A.axis] == 0 && !lv.padded()) ? Space::Line : Space::Full;
+    }
+}
+
+// Decide whether elementwise node `id` can be evaluated inside an existing open region.
+bool Planner::try_join(NodeId id, int* rid_out, bool* line_pos) {
+  const Node& n = g_.node(id);
+  int rid = -1;
+  // position of node n in region R: FULL (shape S), LINE (S without the axis) or neither
+  auto full_pos = [&](const Region& R) {
+    return n.shape == R.S || (n.shape.empty() && R.S == Shape{1} && R.axis < 0);
+  };
+  auto line_pos_of = [&](const Region& R) {
+    return !full_pos(R) && R.axis >= 0 && n.shape == drop_axis(R.S, R.axis);
+  };
+  for (NodeId s : n.src) {
+    Val& v = vals_[s];
+    if (v.k == Val::Dev) continue;
+    Region& R = P_.regions_[v.region];
+    bool ok = !R.closed;
+    if (ok) {
+      if (full_pos(R)) ok = (v.k == Val::LFull || v.k == Val::LBcast);
+      else if (line_pos_of(R)) ok = (v.k == Val::LLine);
+      else ok = false;
+    }
+    if (!ok) {
+      materialize(s);
+      continue;
+    }
+    if (rid < 0) {
+      rid = v.region;
+    } else if (rid != v.region) {
+      Region& A = P_.regions_[rid];
+      Region& B = P_.regions_[v.region];
+      bool compat = A.S == B.S && (A.axis < 0 || B.axis < 0 || A.axis == B.axis);
+      if (compat) merge_regions(rid, v.region);
+      else materialize(s);
+    }
+  }
+  if (rid < 0) return false;
+  Region& R = P_.regions_[rid];
+  *line_pos = line_pos_of(R);
+  *rid_out = rid;
+  return true;
+}
+
+int Planner::copy_view_to_slot(const View& v, int slot_src, DType dt, NodeId node) {
+  int rid = new_region(v.shape);
+  Region& R = P_.regions_[rid];
+  R.name = "copy";
+  View vv = v;
+  if (vv.shape.empty()) { vv.shape = {1}; vv.strides = {0}; }
+  int ln = add_leaf(rid, slot_src, vv, dt);
+  (void)node;
+  int slot = output_slot(rid, ln);
+  close_region(rid);
+  return slot;
+}
+
+void Planner::visit_elementwise(NodeId id) {
+  const Node& n = g_.node(id);
+  int rid;
+  bool line_pos = false;
+  if (!try_join(id, &rid, &line_pos)) {
+    rid = new_region(n.shape);
+    line_pos = false;
+  }
+  RNode rn;
+  rn.kind = (int)n.op.kind;
+  rn.dtype = n.dtype;
+  rn.to = n.op.to;
+  rn.space = line_pos ? Space::Line : Space::Full;
+  for (NodeId s : n.src) rn.in.push_back(region_operand(rid, s, line_pos));
+  // A FULL-position op whose operands are all line values is itself a line value
+  // broadcast along the axis: compute it once per line instead of per element.
+  bool hoist = false;
+  if (!line_pos && P_.regions_[rid].axis >= 0) {
+    hoist = true;
+    for (int i : rn.in)
+      if (P_.regions_[rid].nodes[i].space != Space::Line) hoist = false;
+    if (hoist) rn.space = Space::Line;
+  }
+  int r = add_node(rid, rn);
+  Val v;
+  v.region = rid;
+  v.rn = r;
+  v.k = line_pos ? Val::LLine : (hoist ? Val::LBcast : Val::LFull);
+  vals_[id] = v;
+}
+
+void Planner::visit_movement(NodeId id) {
+  const Node& n = g_.node(id);
+  NodeId s = n.src[0];
+  Val& a = vals_[s];
+  if (a.k != Val::Dev) {
+    Region& R = P_.regions_[a.region];
+    const Shape& is = g_.shape(s);
+    if ((n.op.kind == OpKind::Reshape || n.op.kind == OpKind::Expand) && n.shape == is) {
+      vals_[id] = a;
+      return;
+    }
+    if (!R.closed && R.axis >= 0) {
+      if (n.op.kind == OpKind::Reshape && a.k == Val::LLine && n.shape == keep_axis(R.S, R.axis)) {
+        vals_[id] = a;
+        vals_[id].k = Val::LKeep;
+        return;
+      }
+      if (n.op.kind == OpKind::Reshape && a.k == Val::LKeep && n.shape == drop_axis(R.S, R.axis)) {
+        vals_[id] = a;
+        vals_[id].k = Val::LLine;
+        return;
+      }
+      if (n.op.kind == OpKind::Expand && a.k == Val::LKeep && n.shape == R.S) {
+        vals_[id] = a;
+        vals_[id].k = Val::LBcast;
+        return;
+      }
+    }
+    materialize(s);
+  }
+  Val& d = vals_[s];
+  View v = d.view;
+  int slot = d.slot;
+  if (v.padded() && n.op.kind != OpKind::Reshape) {
+    slot = copy_view_to_slot(v, slot, n.dtype, s);
+    v = View::contiguous(g_.shape(s));
+  }
+  View r;
+  switch (n.op.kind) {
+    case OpKind::Reshape:
+      if (!view_reshape(v, n.shape, &r)) {
+        slot = copy_view_to_slot(v, slot, n.dtype, s);
+        r = View::contiguous(n.shape);
+      }
+      break;
+    case OpKind::Expand: r = view_expand(v, n.shape); break;
+    case OpKind::Permute: r = view_permute(v, n.op.perm); break;
+    case OpKind::Slice: r = view_slice(v, n.op.ranges); break;
+    case OpKind::Flip: r = view_flip(v, n.op.axes); break;
+    case OpKind::Pad: r = view_pad(v, n.op.pads); break;
+    default: throw Error("planner: not a movement op");
+  }
+  Val out;
+  out.k = Val::Dev;
+  out.slot = slot;
+  out.view = r;
+  vals_[id] = out;
+}
+
+void Planner::visit_reduce(NodeId id) {
+  const Node& n = g_.node(id);
+  NodeId s = n.src[0];
+  int axis = (int)n.op.axis;
+  Val& a = vals_[s];
+  int rid = -1;
+  if (a.k == Val::LFull) {
+    Region& R = P_.regions_[a.region];
+    if (!R.closed && R.S == g_.shape(s) && (R.axis < 0 || R.axis == axis)) rid = a.region;
+    else materialize(s);
+  } else if (a.k != Val::Dev) {
+    materialize(s);
+  }
+  if (rid < 0) {
+    rid = new_region(g_.shape(s));
+  }
+  Region& R = P_.regions_[rid];
+  if (R.axis < 0) {
+    R.axis = axis;
+    for (auto& nn : R.nodes)
+      if (nn.kind == RK_LEAF) {
+        const View& lv = R.leaves[nn.leaf].view;
+        nn.space = (lv.strides[axis] == 0 && !lv.padded()) ? Space::Line : Space::Full;
+      }
+  }
+  int in = region_operand(rid, s, false);
+  RNode rn;
+  rn.kind = (int)n.op.kind;
+  rn.dtype = n.dtype;
+  rn.space = Space::Line;
+  rn.arg = n.op.arg;
+  rn.in = {in};
+  int r = add_node(rid, rn);
+  Val v;
+  v.k = Val::LLine;
+  v.region = rid;
+  v.rn = r;
+  vals_[id] = v;
+}
+
+// Softmax / RmsNorm: a row program inside a line region (interp/nn.rs:18-120).
+void Planner::visit_rowop(NodeId id) {
+  const Node& n = g_.node(id);
+  NodeId s = n.src[0];
+  int axis = (int)n.op.axis;
+  Val& a = vals_[s];
+  int rid = -1;
+  if (a.k == Val::LFull) {
+    Region& R = P_.regions_[a.region];
+    if (!R.closed && R.S == g_.shape(s) && (R.axis < 0 || R.axis == axis)) rid = a.region;
+    else materialize(s);
+  } else if (a.k != Val::Dev) {
+    materialize(s);
+  }
+  if (rid < 0) rid = new_region(g_.shape(s));
+  {
+    Region& R = P_.regions_[rid];
+    if (R.axis < 0) {
+      R.axis = axis;
+      for (auto& nn : R.nodes)
+        if (nn.kind == RK_LEAF) {
+          const View& lv = R.leaves[nn.leaf].view;
+          nn.space = (lv.strides[axis] == 0 && !lv.padded()) ? Space::Line : Space::Full;
+        }
+    }
+  }
+  DType dt = n.dtype;
+  DType acc = dt == DType::F64 ? DType::F64 : DType::F32;
+  int x = region_operand(rid, s, false);
+  auto mk = [&](int kind, DType d, Space sp, std::vector<int> in) {
+    RNode r;
+    r.kind = kind;
+    r.dtype = d;
+    r.space = sp;
+    r.to = d;
+    r.in = std::move(in);
+    return add_node(rid, r);
+  };
+  int xf = (dt == acc) ? x : mk((int)OpKind::Cast, acc, Space::Full, {x});
+  int y;
+  if (n.op.kind == OpKind::Softmax) {
+    int m = mk((int)OpKind::ReduceMax, acc, Space::Line, {xf});
+    int nm = mk((int)OpKind::Neg, acc, Space::Line, {m});
+    int d = mk((int)OpKind::Add, acc, Space::Full, {xf, nm});
+    int e = mk(RK_EXP, acc, Space::Full, {d});
+    int sm = mk((int)OpKind::Sum, acc, Space::Line, {e});
+    y = mk(RK_DIV, acc, Space::Full, {e, sm});
+  } else {
+    int sq = mk((int)OpKind::Mul, acc, Space::Full, {xf, xf});
+    int ss = mk((int)OpKind::Sum, acc, Space::Line, {sq});
+    RNode rr;
+    rr.kind = RK_SQRT_ADD_EPS;
+    rr.dtype = acc;
+    rr.space = Space::Line;
+    rr.in = {ss};
+    rr.eps = n.op.eps;
+    rr.axis = g_.shape(s)[axis];
+    int rms = add_node(rid, rr);
+    y = mk(RK_DIV, acc, Space::Full, {xf, rms});
+  }
+  int out = (dt == acc) ? y : mk((int)OpKind::Cast, dt, Space::Full, {y});
+  Val v;
+  v.k = Val::LFull;
+  v.region = rid;
+  v.rn = out;
+  vals_[id] = v;
+}
+
+// ---------------- contraction ----------------
+
+namespace {
+// Merge `axes` (in the given order) of a view into one (stride, size). False if not dense.
+bool merge_axes(const View& v, const std::vector<size_t>& axes, int64_t* stride, int64_t* size) {
+  int64_t sz = 1, st = 0;
+  bool have = false;
+  for (size_t i = axes.size(); i-- > 0;) {
+    size_t a = axes[i];
+    if (v.shape[a] == 1) continue;
+    if (!have) {
+      st = v.strides[a];
+      have = true;
+    } else if (v.strides[a] != st * sz) {
+      return false;
+    }
+    sz *= (int64_t)v.shape[a];
+  }
+  *stride = have ? st : 0;
+  *size = sz;
+  if (!have) {
+    for (size_t a : axes) sz *= (int64_t)v.shape[a];
+    *size = sz;
+  }
+  return true;
+}
+}  // namespace
+
+void Planner::visit_dot(NodeId id) {
+  const Node& n = g_.node(id);
+  NodeId an = n.src[0], bn = n.src[1];
+  GemmStep G;
+  auto fp8 = fp8_pat_.find(id);
+  NodeId out_node = id;
+  if (fp8 != fp8_pat_.end()) {
+    an = fp8->second.xq;
+    bn = fp8->second.wq;
+  }
+  View av = dev_view_of(an), bv = dev_view_of(bn);
+  int aslot = vals_[an].slot, bslot = vals_[bn].slot;
+  DType in_dt = g_.dtype(an);
+  const Op& op = n.op;
+  std::vector<size_t> afree = free_axes(av.shape.size(), op.lb, op.lc);
+  std::vector<size_t> bfree = free_axes(bv.shape.size(), op.rb, op.rc);
+  int64_t sab, bsz, sam, m, sak, k, sbb, bsz2, sbn, nn, sbk, k2;
+  bool ok = merge_axes(av, op.lb, &sab, &bsz) && merge_axes(av, afree, &sam, &m) && merge_axes(av, op.lc, &sak, &k);
+  bool okb = merge_axes(bv, op.rb, &sbb, &bsz2) && merge_axes(bv, bfree, &sbn, &nn) && merge_axes(bv, op.rc, &sbk, &k2);
+  auto canon = [&](NodeId x, View& v, int& slot, const std::vector<size_t>& order) {
+    View p = view_permute(v, order);
+    slot = copy_view_to_slot(p, slot, g_.dtype(x), x);
+    v = View::contiguous(p.shape);
+  };
+  // A must be k-contiguous (or trivially so) for every kernel family; canonicalise otherwise.
+  if (!ok || (k > 1 && sak != 1)) {
+    std::vector<size_t> order(op.lb);
+    order.insert(order.end(), afree.begin(), afree.end());
+    order.insert(order.end(), op.lc.begin(), op.lc.end());
+    canon(an, av, aslot, order);
+    std::vector<size_t> b0, f0, c0;
+    size_t t = 0;
+    for (size_t i = 0; i < op.lb.size(); ++i) b0.push_back(t++);
+    for (size_t i = 0; i < afree.size(); ++i) f0.push_back(t++);
+    for (size_t i = 0; i < op.lc.size(); ++i) c0.push_back(t++);
+    merge_axes(av, b0, &sab, &bsz);
+    merge_axes(av, f0, &sam, &m);
+    merge_axes(av, c0, &sak, &k);
+  }
+  // B: k-contiguous ([n][k]) or n-contiguous ([k][n]) are native; else make it [b][n][k].
+  if (!okb || !((k2 <= 1 || sbk == 1) || (nn <= 1 || sbn == 1))) {
+    std::vector<size_t> order(op.rb);
+    order.insert(order.end(), bfree.begin(), bfree.end());
+    order.insert(order.end(), op.rc.begin(), op.rc.end());
+    canon(bn, bv, bslot, order);
+    std::vector<size_t> b0, f0, c0;
+    size_t t = 0;
+    for (size_t i = 0; i < op.rb.size(); ++i) b0.push_back(t++);
+    for (size_t i = 0; i < bfree.size(); ++i) f0.push_back(t++);
+    for (size_t i = 0; i < op.rc.size(); ++i) c0.push_back(t++);
+    merge_axes(bv, b0, &sbb, &bsz2);
+    merge_axes(bv, f0, &sbn, &nn);
+    merge_axes(bv, c0, &sbk, &k2);
+  }
+  G.a_slot = aslot;
+  G.b_slot = bslot;
+  G.a_off = av.offset;
+  G.b_off = bv.offset;
+  G.sab = sab; G.sam = sam; G.sak = (k <= 1 ? 1 : sak);
+  G.sbb = sbb; G.sbk = sbk; G.sbn = sbn;
+  if (k2 <= 1) G.sbk = 1;
+  if (nn <= 1 && G.sbk != 1) G.sbn = 1;
+  G.batch = (size_t)bsz;
+  G.m = (size_t)m;
+  G.n = (size_t)nn;
+  G.k = (size_t)k;
+  G.in_dtype = in_dt;
+  G.out_dtype = n.dtype;
+  DType out_dt = n.dtype;
+  if (fp8 != fp8_pat_.end()) {
+    out_node = fp8->first == id ? id : id;
+    // epilogue scales
+    View sxv = dev_view_of(fp8->second.sx);
+    View swv = dev_view_of(fp8->second.sw);
+    if (vals_[fp8->second.sx].view.padded() || swv.padded()) throw Error("planner: padded fp8 scales");
+    G.alpha_slot = vals_[fp8->second.sx].slot;
+    G.alpha_off = sxv.offset;
+    G.col_scale_slot = vals_[fp8->second.sw].slot;
+    G.col_scale_off = swv.offset;
+    G.col_scale_stride = swv.strides.empty() ? 1 : swv.strides.back();
+    G.out_dtype = g_.dtype(fp8->second.dot);  // final cast dtype recorded as dot key
+    out_dt = G.out_dtype;
+  }
+  int cslot = new_slot(SlotKind::Temp, out_dt, G.batch * G.m * G.n * dt_width(out_dt), id);
+  G.c_slot = cslot;
+  P_.gemms_.push_back(G);
+  int step = new_step(Step::GEMM, (int)P_.gemms_.size() - 1, "gemm");
+  depend(step, G.a_slot);
+  depend(step, G.b_slot);
+  if (G.alpha_slot >= 0) depend(step, G.alpha_slot);
+  if (G.col_scale_slot >= 0) depend(step, G.col_scale_slot);
+  slot_producer_[cslot] = step;
+  Val v;
+  v.k = Val::Dev;
+  v.slot = cslot;
+  v.view = View::contiguous(n.shape);
+  NodeId target = id;
+  if (fp8 != fp8_pat_.end()) target = fp8->second.dot;  // the pattern's final node
+  vals_[target] = v;
+  if (target != id) vals_[target].view = View::contiguous(g_.shape(target));
+}
+
+void Planner::visit_sdpa(NodeId id) {
+  const Node& n = g_.node(id);
+  AttnPattern pat;
+  auto it = attn_pat_.find(id);
+  if (it != attn_pat_.end()) {
+    pat = it->second;
+  } else {
+    pat.q = n.src[0];
+    pat.k = n.src[1];
+    pat.v = n.src[2];
+    pat.causal = n.op.causal;
+    pat.scale = 1.0f / std::sqrt((float)g_.shape(pat.q).back());
+  }
+  const Shape& qs = g_.shape(pat.q);
+  size_t r = qs.size();
+  AttnStep A;
+  A.s = qs[r - 2];
+  A.d = qs[r - 1];
+  A.bh = numel(qs) / (A.s * A.d);
+  A.scale = pat.scale;
+  A.causal = pat.causal;
+  A.dtype = g_.dtype(pat.q);
+  AttnArgs probe;
+  probe.bh = (int64_t)A.bh;
+  probe.s = (int64_t)A.s;
+  probe.d = (int64_t)A.d;
+  probe.dtype = (int)A.dtype;
+  probe.causal = A.causal;
+  if (!attn_supported(probe) || g_.shape(pat.k) != qs || g_.shape(pat.v) != qs)
+    throw Error("kurumi_hip: attention shape/dtype not supported by the flash kernel: " + shape_str(qs) + " " +
+                dt_name(A.dtype));
+  int slots[3];
+  NodeId ins[3] = {pat.q, pat.k, pat.v};
+  for (int i = 0; i < 3; ++i) {
+    View v = dev_view_of(ins[i]);
+    slots[i] = vals_[ins[i]].slot;
+    if (!v.is_contiguous()) {
+      slots[i] = copy_view_to_slot(v, slots[i], g_.dtype(ins[i]), ins[i]);
+    }
+  }
+  A.q_slot = slots[0];
+  A.k_slot = slots[1];
+  A.v_slot = slots[2];
+  A.o_slot = new_slot(SlotKind::Temp, A.dtype, numel(qs) * dt_width(A.dtype), id);
+  P_.attns_.push_back(A);
+  int step = new_step(Step::ATTN, (int)P_.attns_.size() - 1, "attention");
+  for (int s : slots) depend(step, s);
+  slot_producer_[A.o_slot] = step;
+  Val v;
+  v.k = Val::Dev;
+  v.slot = A.o_slot;
+  v.view = View::contiguous(n.shape);
+  vals_[id] = v;
+}
+
+// ---------------- pattern pre-pass ----------------
+
+// Decomposed attention (graph/ops/nn/attention.rs:97-113):
+//   raw = dot(q,k; lc=[r-1], rc=[r-1], batch) ; sc = raw * scalar(c) ; [sc += cast(expand(reshape(causal)))]
+//   p = softmax(sc, r-1) ; out = dot(p, v; lc=[r-1], rc=[r-2], batch)
+bool Planner::match_attention(NodeId d2) {
+  const Node& n2 = g_.node(d2);
+  if (n2.op.kind != OpKind::DotGeneral) return false;
+  size_t r = n2.shape.size();
+  if (r < 2) return false;
+  std::vector<size_t> batch;
+  for (size_t i = 0; i + 2 < r; ++i) batch.push_back(i);
+  auto single = [&](NodeId x) { return consumers_[x] == 1 && !root_set_.count(x); };
+  if (n2.op.lc != std::vector<size_t>{r - 1} || n2.op.rc != std::vector<size_t>{r - 2} || n2.op.lb != batch ||
+      n2.op.rb != batch)
+    return false;
+  NodeId p = n2.src[0], v = n2.src[1];
+  const Node& sm = g_.node(p);
+  if (sm.op.kind != OpKind::Softmax || sm.op.axis != r - 1 || !single(p)) return false;
+  NodeId sc = sm.src[0];
+  if (!single(sc)) return false;
+  std::vector<NodeId> absorbed = {p, sc};
+  bool causal = false;
+  const Node* mul = &g_.node(sc);
+  if (mul->op.kind == OpKind::Add) {
+    // one operand is the causal bias
+    NodeId x0 = mul->src[0], b0 = mul->src[1];
+    auto is_bias = [&](NodeId b, std::vector<NodeId>& chain) {
+      NodeId cur = b;
+      if (g_.node(cur).op.kind == OpKind::Cast) { if (!single(cur)) return false; chain.push_back(cur); cur = g_.node(cur).src[0]; }
+      if (g_.node(cur).op.kind != OpKind::Expand || !single(cur)) return false;
+      chain.push_back(cur);
+      cur = g_.node(cur).src[0];
+      if (g_.node(cur).op.kind != OpKind::Reshape || !single(cur)) return false;
+      chain.push_back(cur);
+      cur = g_.node(cur).src[0];
+      const Node& c = g_.node(cur);
+      if (c.op.kind != OpKind::Const || c.op.data_dtype != DType::F32 || c.shape.size() != 2 || c.shape[0] != c.shape[1])
+        return false;
+      size_t S = c.shape[0];
+      const float* d = reinterpret_cast<const float*>(c.op.data->data());
+      for (size_t i = 0; i < S; ++i)
+        for (size_t j = 0; j < S; ++j) {
+          float want = j > i ? -INFINITY : 0.f;
+          if (!(d[i * S + j] == want)) return false;
+        }
+      return true;
+    };
+    std::vector<NodeId> chain;
+    if (is_bias(b0, chain)) {
+    } else {
+      chain.clear();
+      if (!is_bias(x0, chain)) return false;
+      std::swap(x0, b0);
+    }
+    causal = true;
+    absorbed.insert(absorbed.end(), chain.begin(), chain.end());
+    if (!single(x0)) return false;
+    absorbed.push_back(x0);
+    mul = &g_.node(x0);
+  }
+  if (mul->op.kind != OpKind::Mul) return false;
+  NodeId raw = mul->src[0], scn = mul->src[1];
+  double c;
+  auto scalar_of = [&](NodeId e, double* out) {
+    const Node& en = g_.node(e);
+    if (en.op.kind != OpKind::Expand) return false;
+    return const_uniform_value(g_.node(en.src[0]), out);
+  };
+  if (!scalar_of(scn, &c)) {
+    std::swap(raw, scn);
+    if (!scalar_of(scn, &c)) return false;
+  }
+  absorbed.push_back(scn);
+  const Node& d1 = g_.node(raw);
+  if (d1.op.kind != OpKind::DotGeneral || !single(raw)) return false;
+  if (d1.op.lc != std::vector<size_t>{r - 1} || d1.op.rc != std::vector<size_t>{r - 1} || d1.op.lb != batch ||
+      d1.op.rb != batch)
+    return false;
+  absorbed.push_back(raw);
+  NodeId q = d1.src[0], k = d1.src[1];
+  if (g_.shape(q) != g_.shape(k) || g_.shape(q) != g_.shape(v)) return false;
+  AttnArgs probe;
+  const Shape& qs = g_.shape(q);
+  probe.s = (int64_t)qs[r - 2];
+  probe.d = (int64_t)qs[r - 1];
+  probe.bh = (int64_t)(numel(qs) / (qs[r - 2] * qs[r - 1]));
+  probe.dtype = (int)g_.dtype(q);
+  probe.causal = causal;
+  if (!attn_supported(probe)) return false;
+  for (NodeId a : absorbed) absorbed_[a] = true;
+  attn_pat_[d2] = AttnPattern{q, k, v, (float)c, causal};
+  return true;
+}
+
+// fp8 quantized linear (the graph the fp8 mixed-precision pass emits):
+//   y = cast_out( mul( mul( dot(cast_f32(xq:f8), cast_f32(wq:f8); lc=[1], rc=[1]), bcast(sx) ), bcast_rows(sw) ) )
+bool Planner::match_fp8_epilogue(NodeId castn) {
+  const Node& cn = g_.node(castn);
+  if (cn.op.kind != OpKind::Cast) return false;
+  auto single = [&](NodeId x) { return consumers_[x] == 1 && !root_set_.count(x); };
+  NodeId m2 = cn.src[0];
+  if (g_.node(m2).op.kind != OpKind::Mul || !single(m2)) return false;
+  auto bcast_src = [&](NodeId e, Shape* src_shape) -> long {
+    const Node& en = g_.node(e);
+    if (en.op.kind != OpKind::Expand || !single(e)) return -1;
+    const Node& rn = g_.node(en.src[0]);
+    if (rn.op.kind != OpKind::Reshape || !single(en.src[0])) return -1;
+    *src_shape = g_.shape(rn.src[0]);
+    return (long)rn.src[0];
+  };
+  auto split = [&](NodeId mul, NodeId* other, NodeId* vec, Shape* vs) {
+    const Node& mn = g_.node(mul);
+    for (int t = 0; t < 2; ++t) {
+      long s = bcast_src(mn.src[1 - t], vs);
+      if (s >= 0) { *other = mn.src[t]; *vec = (NodeId)s; return true; }
+    }
+    return false;
+  };
+  NodeId m1, sw, sx, dot;
+  Shape sws, sxs;
+  if (!split(m2, &m1, &sw, &sws)) return false;
+  if (g_.node(m1).op.kind != OpKind::Mul || !single(m1)) return false;
+  if (!split(m1, &dot, &sx, &sxs)) return false;
+  const Node& dn = g_.node(dot);
+  if (dn.op.kind != OpKind::DotGeneral || !single(dot) || dn.shape.size() != 2) return false;
+  if (dn.op.lc != std::vector<size_t>{1} || dn.op.rc != std::vector<size_t>{1} || !dn.op.lb.empty()) return false;
+  size_t N = dn.shape[1];
+  if (numel(sxs) != 1 || g_.dtype(sx) != DType::F32) return false;
+  if (!(sws == Shape{N} || sws == Shape{1, N}) || g_.dtype(sw) != DType::F32) return false;
+  if (dn.dtype != DType::F32) return false;
+  NodeId ca = dn.src[0], cb = dn.src[1];
+  const Node &can = g_.node(ca), &cbn = g_.node(cb);
+  if (can.op.kind != OpKind::Cast || cbn.op.kind != OpKind::Cast) return false;
+  NodeId xq = can.src[0], wq = cbn.src[0];
+  if (g_.dtype(xq) != DType::F8E4M3 || g_.dtype(wq) != DType::F8E4M3) return false;
+  DType od = cn.op.to;
+  if (od != DType::BF16 && od != DType::F16 && od != DType::F32) return false;
+  // absorb the epilogue chain; the dot visit produces the cast's value
+  std::vector<NodeId> ab = {m2, m1, g_.node(m2).src[0] == m1 ? g_.node(m2).src[1] : g_.node(m2).src[0]};
+  for (NodeId x : ab) absorbed_[x] = true;
+  // the broadcast chains of sx/sw
+  for (NodeId mul : {m1, m2}) {
+    const Node& mn = g_.node(mul);
+    for (NodeId s : mn.src) {
+      if (g_.node(s).op.kind == OpKind::Expand && s != dot && s != m1) {
+        absorbed_[s] = true;
+        absorbed_[g_.node(s).src[0]] = true;
+      }
+    }
+  }
+  if (single(ca)) absorbed_[ca] = true;
+  if (single(cb)) absorbed_[cb] = true;
+  absorbed_[castn] = true;
+  fp8_pat_[dot] = Fp8Pattern{castn, xq, wq, sx, sw};
+  return true;
+}
+
+void Planner::find_patterns() {
+  auto order = reachable_multi(g_, P_.roots_);
+  consumers_.assign(g_.size(), 0);
+  for (NodeId id : order)
+    for (NodeId s : g_.node(id).src) consumers_[s]++;
+  absorbed_.assign(g_.size(), false);
+  for (NodeId id : order) {
+    const OpKind k = g_.node(id).op.kind;
+    if (k == OpKind::DotGeneral && !absorbed_[id]) match_attention(id);
+    if (k == OpKind::Cast && !absorbed_[id]) match_fp8_epilogue(id);
+  }
+}
+
+void Planner::visit(NodeId id) {
+  const Node& n = g_.node(id);
+  switch (n.op.kind) {
+    case OpKind::Input: {
+      auto it = P_.input_slots_.find(id);
+      int slot;
+      if (it == P_.input_slots_.end()) {
+        slot = new_slot(SlotKind::Input, n.dtype, numel(n.shape) * dt_width(n.dtype), id);
+        P_.input_slots_[id] = slot;
+      } else {
+        slot = it->second;
+      }
+      Val v;
+      v.k = Val::Dev;
+      v.slot = slot;
+      v.view = View::contiguous(n.shape);
+      vals_[id] = v;
+      return;
+    }
+    case OpKind::Const: {
+      int slot = new_slot(SlotKind::Const, n.dtype, numel(n.shape) * dt_width(n.dtype), id);
+      Val v;
+      v.k = Val::Dev;
+      v.slot = slot;
+      v.view = View::contiguous(n.shape);
+      vals_[id] = v;
+      return;
+    }
+    case OpKind::Detach:
+      vals_[id] = vals_[n.src[0]];
+      return;
+    case OpKind::Iota:
+    case OpKind::RandUniform: {
+      int rid = new_region(n.shape);
+      RNode rn;
+      rn.kind = (int)n.op.kind;
+      rn.dtype = n.dtype;
+      rn.axis = n.op.axis;
+      rn.space = Space::Full;
+      if (n.op.kind == OpKind::RandUniform) {
+        NodeId s = n.src[0];
+        View sv = dev_view_of(s);
+        View u = sv;
+        if (!view_reshape(sv, Shape{1}, &u)) throw Error("planner: rand seed must be a single element");
+        View lv;
+        lv.shape = P_.regions_[rid].S;
+        lv.strides.assign(lv.shape.size(), 0);
+        lv.offset = u.offset;
+        rn.in = {add_leaf(rid, vals_[s].slot, lv, g_.dtype(s))};
+      }
+      int r = add_node(rid, rn);
+      Val v;
+      v.k = Val::LFull;
+      v.region = rid;
+      v.rn = r;
+      vals_[id] = v;
+      return;
+    }
+    case OpKind::Sum: case OpKind::Prod: case OpKind::ReduceMax: case OpKind::ArgReduce:
+      if (numel(g_.shape(n.src[0])) == 0) throw Error("kurumi_hip: reduction over an empty tensor");
+      visit_reduce(id);
+      return;
+    case OpKind::Softmax: case OpKind::RmsNorm:
+      visit_rowop(id);
+      return;
+    case OpKind::Reshape: case OpKind::Expand: case OpKind::Permute: case OpKind::Slice: case OpKind::Flip:
+    case OpKind::Pad:
+      visit_movement(id);
+      return;
+    case OpKind::DotGeneral:
+      if (attn_pat_.count(id)) { visit_sdpa(id); return; }
+      visit_dot(id);
+      return;
+    case OpKind::Sdpa:
+      visit_sdpa(id);
+      return;
+    default:
+      if (is_elementwise(n.op.kind)) {
+        if (dt_is_complex(n.dtype) || (n.src.size() && dt_is_complex(g_.dtype(n.src[0]))))
+          throw Error("kurumi_hip: complex dtypes are not supported on device");
+        visit_elementwise(id);
+        return;
+      }
+      throw Error(std::string("kurumi_hip: op ") + op_name(n.op.kind) + " is not supported on device");
+  }
+}
+
+void Planner::run() {
+  const auto& roots = P_.roots_;
+  for (NodeId r : roots) {
+    if (r >= g_.size()) throw Error("eval: node id " + std::to_string(r) + " out of range");
+    root_set_.insert(r);
+  }
+  find_patterns();
+  vals_.assign(g_.size(), Val{});
+  auto order = reachable_multi(g_, roots);
+  std::sort(order.begin(), order.end());
+  for (NodeId id : order) {
+    if (absorbed_[id]) continue;
+    visit(id);
+  }
+  // roots: contiguous device buffers
+  for (NodeId r : roots) {
+    if (vals_[r].k == Val::None) throw Error("planner: root " + std::to_string(r) + " was not produced");
+    materialize(r);
+    Val& v = vals_[r];
+    if (!v.view.is_contiguous() || P_.slots_[v.slot].kind != SlotKind::Temp) {
+      int s = copy_view_to_slot(v.view.shape.empty() ? View::contiguous({1}) : v.view, v.slot, g_.dtype(r), r);
+      if (v.view.shape.empty()) {
+        View c = v.view;
+        c.shape = {1};
+        c.strides = {0};
+        s = copy_view_to_slot(c, v.slot, g_.dtype(r), r);
+      }
+      v.slot = s;
+      v.view = View::contiguous(g_.shape(r));
+    }
+    P_.root_vals_.push_back({v.slot, v.view});
+  }
+  // execution order: topological over deps, stable by creation
+  int ns = (int)P_.steps_.size();
+  std::vector<int> state(ns, 0);
+  std::function<void(int)> dfs = [&](int s) {
+    if (state[s] == 2) return;
+    if (state[s] == 1) throw Error("planner: dependency cycle");
+    state[s] = 1;
+    for (int d : P_.steps_[s].deps)
+      if (step_alive_[d]) dfs(d);
+    state[s] = 2;
+    P_.order_.push_back(s);
+  };
+  for (int s = 0; s < ns; ++s)
+    if (step_alive_[s] && (P_.steps_[s].type != Step::REGION || !P_.regions_[P_.steps_[s].index].nodes.empty()))
+      dfs(s);
+}
+
+// ======================= plan =======================
+
+Plan::Plan(const Graph& g, const std::vector<NodeId>& roots, Context* ctx, ConstCache* consts)
+    : g_(g), graph_id_(g.id()), roots_(roots), ctx_(ctx) {
+  if (roots.empty()) throw Error("eval: no output nodes");
+  Planner pl(*this, consts);
+  pl.run();
+  compile();
+  if (ctx_) {
+    allocate();
+    for (auto& s : slots_)
+      if (s.kind == SlotKind::Const) {
+        s.buf = consts->get(g, s.node);
+        s.borrowed = true;
+      }
+  }
+}
+
+Plan::~Plan() {
+  if (hexec_) (void)hipGraphExecDestroy(hexec_);
+  if (hgraph_) (void)hipGraphDestroy(hgraph_);
+  if (ctx_) {
+    for (auto& s : slots_)
+      if (!s.borrowed && s.buf.ptr) ctx_->pool().release(s.buf);
+  }
+}
+
+void Plan::compile() {
+  for (int si : order_) {
+    Step& s = steps_[si];
+    if (s.type == Step::REGION) {
+      RegionCode rc = gen_region(regions_[s.index], slots_, s.index);
+      s.grid = rc.grid;
+      s.block = rc.block;
+      s.arg_slots = rc.arg_slots;
+      s.label = rc.entry;
+      sources_.push_back(rc.src);
+      if (ctx_) s.fn = ctx_->modules().get(rc.src, rc.entry);
+    } else if (s.type == Step::GEMM) {
+      const GemmStep& G = gemms_[s.index];
+      GemmArgs a;
+      a.sab = G.sab; a.sam = G.sam; a.sak = G.sak; a.sbb = G.sbb; a.sbk = G.sbk; a.sbn = G.sbn;
+      a.batch = (int64_t)G.batch; a.m = (int64_t)G.m; a.n = (int64_t)G.n; a.k = (int64_t)G.k;
+      a.in_type = (int)G.in_dtype; a.out_type = (int)G.out_dtype;
+      if (G.alpha_slot >= 0) a.alpha = reinterpret_cast<const float*>(16);
+      std::ostringstream o;
+      o << gemm_variant(a) << " b" << G.batch << " m" << G.m << " n" << G.n << " k" << G.k;
+      s.label = o.str();
+    } else {
+      const AttnStep& A = attns_[s.index];
+      AttnArgs a;
+      a.bh = (int64_t)A.bh; a.s = (int64_t)A.s; a.d = (int64_t)A.d; a.causal = A.causal; a.dtype = (int)A.dtype;
+      std::ostringstream o;
+      o << attn_variant(a) << " bh" << A.bh << " s" << A.s << " d" << A.d << (A.causal ? " causal" : "");
+      s.label = o.str();
+    }
+  }
+}
+
+void Plan::allocate() {
+  for (auto& s : slots_)
+    if (s.kind != SlotKind::Const && !s.buf.ptr) s.buf = ctx_->pool().alloc(std::max<size_t>(s.bytes, 1));
+}
+
+std::vector<NodeId> Plan::inputs() const {
+  std::vector<NodeId> r;
+  for (auto& kv : input_slots_) r.push_back(kv.first);
+  return r;
+}
+
+void Plan::feed(NodeId input, const Tensor& t) {
+  auto it = input_slots_.find(input);
+  if (it == input_slots_.end()) return;  // not reachable from the roots
+  const Node& n = g_.node(input);
+  if (t.dtype != n.dtype || t.shape != n.shape)
+    throw Error("feed for input %" + std::to_string(input) + ": got " + dt_name(t.dtype) + shape_str(t.shape) +
+                ", expected " + dt_name(n.dtype) + shape_str(n.shape));
+  Slot& s = slots_[it->second];
+  if (t.bytes.size() != s.bytes) throw Error("feed: byte size mismatch");
+  if (!s.bytes) return;
+  KU_HIP(hipMemcpyAsync(s.buf.ptr, t.bytes.data(), s.bytes, hipMemcpyHostToDevice, ctx_->stream()));
+  ctx_->profile().launches[(int)Kind::Upload]++;
+}
+
+static void* slot_ptr(const std::vector<Slot>& slots, int i) { return slots[i].buf.ptr; }
+
+void Plan::launch_step(const Step& s) {
+  hipStream_t st = ctx_->stream();
+  if (s.type == Step::REGION) {
+    std::vector<void*> ptrs(s.arg_slots.size());
+    std::vector<void*> args(s.arg_slots.size());
+    for (size_t i = 0; i < s.arg_slots.size(); ++i) {
+      ptrs[i] = slot_ptr(slots_, s.arg_slots[i]);
+      args[i] = &ptrs[i];
+    }
+    if (s.grid == 0) return;
+    KU_HIP(hipModuleLaunchKernel(s.fn.fn, s.grid, 1, 1, s.block, 1, 1, 0, st, args.data(), nullptr));
+    ctx_->profile().launches[(int)Kind::Fused]++;
+  } else if (s.type == Step::GEMM) {
+    const GemmStep& G = gemms_[s.index];
+    GemmArgs a;
+    size_t iw = dt_width(G.in_dtype);
+    a.a = static_cast<const char*>(slot_ptr(slots_, G.a_slot)) + G.a_off * (int64_t)iw;
+    a.b = static_cast<const char*>(slot_ptr(slots_, G.b_slot)) + G.b_off * (int64_t)iw;
+    a.c = slot_ptr(slots_, G.c_slot);
+    a.sab = G.sab; a.sam = G.sam; a.sak = G.sak; a.sbb = G.sbb; a.sbk = G.sbk; a.sbn = G.sbn;
+    a.batch = (int64_t)G.batch; a.m = (int64_t)G.m; a.n = (int64_t)G.n; a.k = (int64_t)G.k;
+    a.in_type = (int)G.in_dtype;
+    a.out_type = (int)G.out_dtype;
+    if (G.alpha_slot >= 0) a.alpha = static_cast<const float*>(slot_ptr(slots_, G.alpha_slot)) + G.alpha_off;
+    if (G.col_scale_slot >= 0) {
+      a.col_scale = static_cast<const float*>(slot_ptr(slots_, G.col_scale_slot)) + G.col_scale_off;
+      a.col_scale_stride = G.col_scale_stride;
+    }
+    if (G.batch * G.m * G.n == 0) return;
+    launch_gemm(a, st);
+    ctx_->profile().launches[(int)Kind::Gemm]++;
+  } else {
+    const AttnStep& A = attns_[s.index];
+    AttnArgs a;
+    a.q = slot_ptr(slots_, A.q_slot);
+    a.k = slot_ptr(slots_, A.k_slot);
+    a.v = slot_ptr(slots_, A.v_slot);
+    a.o = slot_ptr(slots_, A.o_slot);
+    a.bh = (int64_t)A.bh; a.s = (int64_t)A.s; a.d = (int64_t)A.d;
+    a.scale = A.scale;
+    a.causal = A.causal;
+    a.dtype = (int)A.dtype;
+    launch_attention(a, st);
+    ctx_->profile().launches[(int)Kind::Attention]++;
+  }
+}
+
+void Plan::launch(bool use_graph) {
+  if (!ctx_) throw Error("plan has no device context");
+  ctx_->make_current();
+  if (use_graph) {
+    if (!hexec_) {
+      hipStream_t st = ctx_->stream();
+      KU_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+      try {
+        for (int si : order_) launch_step(steps_[si]);
+      } catch (...) {
+        hipGraph_t tmp;
+        (void)hipStreamEndCapture(st, &tmp);
+        throw;
+      }
+      KU_HIP(hipStreamEndCapture(st, &hgraph_));
+      KU_HIP(hipGraphInstantiate(&hexec_, hgraph_, nullptr, nullptr, 0));
+    }
+    KU_HIP(hipGraphLaunch(hexec_, ctx_->stream()));
+    return;
+  }
+  for (int si : order_) launch_step(steps_[si]);
+}
+
+void* Plan::output_ptr(size_t i) const { return slots_[root_vals_.at(i).first].buf.ptr; }
+
+Tensor Plan::download(size_t i) {
+  const auto& rv = root_vals_.at(i);
+  NodeId r = roots_.at(i);
+  Tensor t;
+  t.dtype = g_.dtype(r);
+  t.shape = g_.shape(r);
+  t.bytes.resize(numel(t.shape) * dt_width(t.dtype));
+  if (!t.bytes.empty())
+    KU_HIP(hipMemcpyAsync(t.bytes.data(), slots_[rv.first].buf.ptr, t.bytes.size(), hipMemcpyDeviceToHost,
+                          ctx_->stream()));
+  ctx_->sync();
+  ctx_->profile().launches[(int)Kind::Download]++;
+  return t;
+}
+
+std::string Plan::step_label(size_t i) const { return steps_[order_.at(i)].label; }
+
+std::vector<std::string> Plan::sources() const { return sources_; }
+
+std::vector<double> Plan::time_steps(int iters) {
+  if (!ctx_) throw Error("plan has no device context");
+  ctx_->make_current();
+  hipStream_t st = ctx_->stream();
+  size_t n = order_.size();
+  std::vector<hipEvent_t> ev(n + 1);
+  for (auto& e : ev) KU_HIP(hipEventCreate(&e));
+  std::vector<double> acc(n, 0.0);
+  for (int it = 0; it < iters; ++it) {
+    KU_HIP(hipEventRecord(ev[0], st));
+    for (size_t i = 0; i < n; ++i) {
+      launch_step(steps_[order_[i]]);
+      KU_HIP(hipEventRecord(ev[i + 1], st));
+    }
+    KU_HIP(hipEventSynchronize(ev[n]));
+    for (size_t i = 0; i < n; ++i) {
+      float ms = 0.f;
+      KU_HIP(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+      acc[i] += ms;
+    }
+  }
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  for (auto& a : acc) a /= std::max(iters, 1);
+  return acc;
+}
+
+}  // namespace ku::hipbk

@@ -1,0 +1,199 @@
+// Device plan for one set of graph roots: the fusion planner's output and its executor.
+//
+// The planner walks the reachable nodes in id (= topological) order, like the Metal
+// backend's memoised walk (kurumi_metal/src/backend/eval_walk.rs:73-138) and fusion
+// accretion (backend/eval/fused.rs:13-145), but instead of one pointwise tree per kernel it
+// builds *line regions*: elementwise chains, reductions along one axis and the values
+// broadcast back along that axis, all evaluated by one kernel that owns whole lines.
+// `Softmax`, `RmsNorm` and the decomposed softmax chain (interp/nn.rs:18-69,
+// graph/ops/nn/activation.rs:122-129) therefore become a single pass over the data.
+// Contractions and attention become GEMM / flash-attention steps.
+#pragma once
+#include <map>
+#include <memory>
+#include <set>
+#include <string>
+#include <vector>
+
+#include "../ir/graph.h"
+#include "../ir/tensor.h"
+#include "runtime.h"
+
+namespace ku::hipbk {
+
+// Element-strided view of a contiguous device buffer (movement ops compose into it;
+// the reference's `View{base,strides,out_shape}`, kurumi_metal/src/backend/fuse.rs:70-80).
+struct View {
+  Shape shape;
+  std::vector<int64_t> strides;
+  int64_t offset = 0;
+  // zero padding (Pad): coordinate c on axis d reads source c - plo[d] when inside
+  // [0, src_shape[d]), else 0. Empty when the view is not padded.
+  std::vector<int64_t> plo;
+  Shape src_shape;
+  bool padded() const { return !plo.empty(); }
+  static View contiguous(const Shape& s);
+  bool is_contiguous() const;
+};
+bool view_reshape(const View& v, const Shape& to, View* out);
+View view_expand(const View& v, const Shape& to);
+View view_permute(const View& v, const std::vector<size_t>& perm);
+View view_slice(const View& v, const std::vector<SliceRange>& r);
+View view_flip(const View& v, const std::vector<size_t>& axes);
+View view_pad(const View& v, const std::vector<PadRange>& p);
+
+enum class SlotKind { Input, Const, Temp };
+struct Slot {
+  SlotKind kind = SlotKind::Temp;
+  DType dtype = DType::F32;
+  size_t bytes = 0;
+  NodeId node = 0;
+  DevBuf buf;           // owned unless `borrowed`
+  bool borrowed = false;  // const cache buffers belong to the backend
+};
+
+enum class Space : uint8_t { Full, Line };
+
+// Region expression node kinds: graph elementwise ops keep their OpKind value; the
+// reductions are Sum/Prod/ReduceMax/ArgReduce; the rest are internal.
+enum RK : int {
+  RK_LEAF = 1000,    // read of leaf `leaf`
+  RK_DIV,            // a / b (f32/f64 division, Softmax/RmsNorm)
+  RK_EXP,            // natural exp (Softmax)
+  RK_SQRT_ADD_EPS,   // sqrt(a / len + eps) (RmsNorm)
+};
+
+struct RNode {
+  int kind = RK_LEAF;
+  DType dtype = DType::F32;   // value dtype (lowp values are carried as f32, rounded per op)
+  Space space = Space::Full;
+  std::vector<int> in;
+  int leaf = -1;
+  DType to = DType::F32;      // Cast/Bitcast target
+  ArgKind arg = ArgKind::Max;
+  size_t axis = 0;            // Iota axis
+  float eps = 0.f;
+  int level = 0;
+};
+
+struct Leaf {
+  int slot = -1;
+  View view;          // over the region's iteration shape S (LINE leaves: stride 0 on the axis)
+  DType dtype = DType::F32;
+};
+
+struct Region {
+  Shape S;
+  int axis = -1;      // reduction axis; -1 = pure elementwise
+  std::vector<RNode> nodes;
+  std::vector<Leaf> leaves;
+  std::vector<std::pair<int, int>> outputs;  // (rnode, slot)
+  bool closed = false;
+  std::string name;
+};
+
+struct GemmStep {
+  // C[b, m, n] = sum_k A[b, m, k] * B[b, k, n] (+ fp8 epilogue scales), C contiguous.
+  int a_slot = -1, b_slot = -1, c_slot = -1;
+  int64_t a_off = 0, b_off = 0;
+  int64_t sab = 0, sam = 0, sak = 0;   // A strides (elements)
+  int64_t sbb = 0, sbk = 0, sbn = 0;   // B strides
+  size_t batch = 1, m = 0, n = 0, k = 0;
+  DType in_dtype = DType::BF16, out_dtype = DType::BF16;
+  // fp8 epilogue: C = round(acc * (*alpha) * col_scale[n]); alpha/col_scale from slots
+  int alpha_slot = -1, col_scale_slot = -1;
+  int64_t alpha_off = 0, col_scale_off = 0, col_scale_stride = 1;
+  std::string variant;
+};
+
+struct AttnStep {
+  int q_slot = -1, k_slot = -1, v_slot = -1, o_slot = -1;
+  size_t bh = 0, s = 0, d = 0;
+  float scale = 1.f;
+  bool causal = false;
+  DType dtype = DType::BF16;
+};
+
+struct Step {
+  enum Type { REGION, GEMM, ATTN } type;
+  int index;             // into regions / gemms / attns
+  std::set<int> deps;    // producer step ids
+  // compiled launch (regions)
+  KernelFn fn;
+  unsigned grid = 0, block = 0;
+  std::vector<int> arg_slots;
+  std::string label;
+};
+
+class Backend;  // HipBackend (backend.h)
+
+class Plan {
+ public:
+  // Build the plan for `roots` of `g`. Input shapes come from the graph's Input nodes;
+  // `ctx` may be null for a codegen-only plan (no device buffers, no launches).
+  Plan(const Graph& g, const std::vector<NodeId>& roots, Context* ctx, class ConstCache* consts);
+  ~Plan();
+
+  // Upload an Input's host value (must match the declared shape and dtype).
+  void feed(NodeId input, const Tensor& t);
+  // Enqueue every step on the context stream (async). With `graph` true the steps are
+  // recorded once into a hipGraph and replayed on later calls.
+  void launch(bool use_graph = false);
+  Tensor download(size_t i);
+  size_t num_outputs() const { return roots_.size(); }
+  void* output_ptr(size_t i) const;
+
+  // Introspection
+  size_t num_steps() const { return order_.size(); }
+  std::string step_label(size_t i) const;
+  std::vector<std::string> sources() const;
+  // Average GPU ms of each step over `iters` launches, timed with hipEvents on the stream.
+  std::vector<double> time_steps(int iters);
+  std::vector<NodeId> inputs() const;
+
+ private:
+  friend class Planner;
+  void compile();
+  void allocate();
+  void launch_step(const Step& s);
+
+  const Graph& g_;
+  uint64_t graph_id_;
+  std::vector<NodeId> roots_;
+  Context* ctx_;
+  std::vector<Slot> slots_;
+  std::vector<Region> regions_;
+  std::vector<GemmStep> gemms_;
+  std::vector<AttnStep> attns_;
+  std::vector<Step> steps_;
+  std::vector<int> order_;                 // execution order of steps
+  std::map<NodeId, int> input_slots_;
+  std::vector<std::pair<int, View>> root_vals_;  // slot + view of each root
+  std::vector<std::string> sources_;
+  hipGraph_t hgraph_ = nullptr;
+  hipGraphExec_t hexec_ = nullptr;
+};
+
+// Backend-owned cache of uploaded constants keyed by (graph id, node)
+// (kurumi_metal/src/backend.rs:23-26, eval_walk.rs:99-114).
+class ConstCache {
+ public:
+  explicit ConstCache(Context* ctx) : ctx_(ctx) {}
+  ~ConstCache();
+  DevBuf get(const Graph& g, NodeId id);
+  void drop_graph(uint64_t gid);
+
+ private:
+  Context* ctx_;
+  std::map<std::pair<uint64_t, NodeId>, DevBuf> map_;
+};
+
+// Generated-source entry points (codegen.cpp)
+struct RegionCode {
+  std::string src, entry;
+  unsigned grid = 0, block = 0;
+  std::vector<int> arg_slots;  // leaf/output slots in kernel parameter order
+};
+RegionCode gen_region(const Region& r, const std::vector<Slot>& slots, int index);
+
+}  // namespace ku::hipbk

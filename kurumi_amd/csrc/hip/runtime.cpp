@@ -1,0 +1,206 @@
+#include "runtime.h"
+
+#include <hip/hiprtc.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+
+namespace ku::hipbk {
+
+void hip_check(hipError_t e, const char* what, const char* file, int line) {
+  if (e == hipSuccess) return;
+  std::ostringstream o;
+  o << "HIP error " << hipGetErrorName(e) << " (" << hipGetErrorString(e) << ") at " << file << ":" << line << ": "
+    << what;
+  throw Error(o.str());
+}
+
+// ---------------- pool ----------------
+
+size_t Pool::bucket(size_t bytes) {
+  if (bytes == 0) bytes = 1;
+  if (bytes <= (1u << 20)) return (bytes + 255) & ~size_t(255);
+  // 1/8-octave buckets above 1 MiB
+  size_t p = 1;
+  while ((p << 1) <= bytes) p <<= 1;
+  size_t step = p / 8;
+  return (bytes + step - 1) / step * step;
+}
+
+DevBuf Pool::alloc(size_t bytes) {
+  size_t b = bucket(bytes);
+  auto it = free_.find(b);
+  if (it != free_.end()) {
+    DevBuf d{it->second, b};
+    free_.erase(it);
+    cached_ -= b;
+    live_ += b;
+    return d;
+  }
+  void* p = nullptr;
+  hipError_t e = hipMalloc(&p, b);
+  if (e != hipSuccess) {
+    // release cached buffers and retry once
+    (void)hipGetLastError();
+    trim();
+    KU_HIP(hipMalloc(&p, b));
+  }
+  live_ += b;
+  return DevBuf{p, b};
+}
+
+void Pool::release(DevBuf d) {
+  if (!d.ptr) return;
+  live_ -= d.bytes;
+  cached_ += d.bytes;
+  free_.emplace(d.bytes, d.ptr);
+}
+
+void Pool::trim() {
+  for (auto& kv : free_) (void)hipFree(kv.second);
+  free_.clear();
+  cached_ = 0;
+}
+
+Pool::~Pool() { trim(); }
+
+// ---------------- rtc ----------------
+
+static uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ull) {
+  for (unsigned char c : s) {
+    h ^= c;
+    h *= 1099511628211ull;
+  }
+  return h;
+}
+
+static const char* kRtcOpts[] = {"--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang", "-target-feature",
+                                 "-Xclang", "-packed-fp32-ops", "-fno-fast-math"};
+static constexpr int kNumRtcOpts = sizeof(kRtcOpts) / sizeof(kRtcOpts[0]);
+
+std::string rtc_cache_dir() {
+  if (const char* d = std::getenv("KURUMI_HIP_CACHE")) return d;
+  if (const char* h = std::getenv("HOME")) return std::string(h) + "/.cache/kurumi_hip";
+  return "/tmp/kurumi_hip_cache";
+}
+
+static void mkdirs(const std::string& path) {
+  std::string cur;
+  for (size_t i = 0; i < path.size(); ++i) {
+    cur.push_back(path[i]);
+    if (path[i] == '/' || i + 1 == path.size()) ::mkdir(cur.c_str(), 0755);
+  }
+}
+
+std::vector<char> rtc_compile(const std::string& src, const std::string& name_hint) {
+  std::string key;
+  for (int i = 0; i < kNumRtcOpts; ++i) key += kRtcOpts[i], key += ' ';
+  int ver_major = 0, ver_minor = 0;
+  hiprtcVersion(&ver_major, &ver_minor);
+  key += std::to_string(ver_major) + "." + std::to_string(ver_minor);
+  char hex[32];
+  std::snprintf(hex, sizeof hex, "%016llx", (unsigned long long)fnv1a(src, fnv1a(key)));
+  bool use_disk = !std::getenv("KURUMI_HIP_NO_DISK_CACHE");
+  std::string dir = rtc_cache_dir();
+  std::string path = dir + "/" + hex + ".co";
+  if (use_disk) {
+    std::ifstream f(path, std::ios::binary);
+    if (f) {
+      std::vector<char> co((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+      if (!co.empty()) return co;
+    }
+  }
+  hiprtcProgram prog;
+  if (hiprtcCreateProgram(&prog, src.c_str(), (name_hint + ".hip").c_str(), 0, nullptr, nullptr) != HIPRTC_SUCCESS)
+    throw Error("hiprtcCreateProgram failed for " + name_hint);
+  hiprtcResult r = hiprtcCompileProgram(prog, kNumRtcOpts, kRtcOpts);
+  if (r != HIPRTC_SUCCESS) {
+    size_t ls = 0;
+    hiprtcGetProgramLogSize(prog, &ls);
+    std::string log(ls, '\0');
+    if (ls) hiprtcGetProgramLog(prog, log.data());
+    hiprtcDestroyProgram(&prog);
+    throw Error("hipRTC compile of " + name_hint + " failed: " + log + "\n--- source ---\n" + src);
+  }
+  size_t cs = 0;
+  hiprtcGetCodeSize(prog, &cs);
+  std::vector<char> co(cs);
+  hiprtcGetCode(prog, co.data());
+  hiprtcDestroyProgram(&prog);
+  if (use_disk) {
+    mkdirs(dir);
+    std::string tmp = path + ".tmp" + std::to_string(::getpid());
+    {
+      std::ofstream f(tmp, std::ios::binary);
+      f.write(co.data(), static_cast<std::streamsize>(co.size()));
+    }
+    std::rename(tmp.c_str(), path.c_str());
+  }
+  return co;
+}
+
+KernelFn ModuleCache::get(const std::string& src, const std::string& entry) {
+  auto it = map_.find(src);
+  if (it != map_.end()) {
+    ++hits_;
+    return it->second;
+  }
+  std::vector<char> co = rtc_compile(src, entry);
+  KernelFn k;
+  KU_HIP(hipModuleLoadData(&k.mod, co.data()));
+  KU_HIP(hipModuleGetFunction(&k.fn, k.mod, entry.c_str()));
+  ++compiled_;
+  map_.emplace(src, k);
+  return k;
+}
+
+ModuleCache::~ModuleCache() {
+  for (auto& kv : map_) (void)hipModuleUnload(kv.second.mod);
+}
+
+const char* kind_name(Kind k) {
+  static const char* n[] = {"fused", "gemm", "attention", "upload", "download"};
+  int i = static_cast<int>(k);
+  return (i >= 0 && i < static_cast<int>(Kind::NumKinds)) ? n[i] : "?";
+}
+
+// ---------------- context ----------------
+
+Context::Context(int device) : device_(device) {
+  if (const char* f = std::getenv("KURUMI_HIP_FORCE_NO_DEVICE"); f && *f && *f != '0')
+    throw Error("no HIP device (KURUMI_HIP_FORCE_NO_DEVICE is set)");
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess || n == 0) {
+    (void)hipGetLastError();
+    throw Error("no HIP device available");
+  }
+  if (device < 0 || device >= n) throw Error("HIP device index out of range");
+  KU_HIP(hipSetDevice(device));
+  hipDeviceProp_t prop;
+  KU_HIP(hipGetDeviceProperties(&prop, device));
+  arch_ = prop.gcnArchName;
+  num_cus_ = prop.multiProcessorCount;
+  if (arch_.rfind("gfx950", 0) != 0) throw Error("kurumi_hip targets gfx950 (MI355X); found " + arch_);
+  KU_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+  if (const char* t = std::getenv("KURUMI_GPUTIME"); t && *t && *t != '0') timing_ = true;
+}
+
+Context::~Context() {
+  if (stream_) {
+    (void)hipSetDevice(device_);
+    (void)hipStreamSynchronize(stream_);
+    (void)hipStreamDestroy(stream_);
+  }
+}
+
+void Context::make_current() const { KU_HIP(hipSetDevice(device_)); }
+
+void Context::sync() { KU_HIP(hipStreamSynchronize(stream_)); }
+
+}  // namespace ku::hipbk

@@ -1,0 +1,34 @@
+// Host tensor value and feeds: the owned, row-major little-endian result the backend
+// seam returns (kurumi_core/src/dtype.rs:178-192 `TensorVal`, backend.rs:12 `Feeds`).
+#pragma once
+#include <cstdint>
+#include <memory>
+#include <unordered_map>
+#include <vector>
+
+#include "dtype.h"
+#include "graph.h"
+
+namespace ku {
+
+struct Tensor {
+  DType dtype = DType::F32;
+  Shape shape;
+  std::vector<uint8_t> bytes;
+  size_t nbytes() const { return bytes.size(); }
+};
+
+using Feeds = std::unordered_map<NodeId, std::shared_ptr<const Tensor>>;
+
+// The backend seam (kurumi_core/src/backend.rs:14-31): evaluate one or several nodes of a
+// borrowed graph with `Input` nodes bound by `feeds`; results are owned host tensors.
+// `eval_many` shares one pass across ids and must equal per-node evaluation.
+class Backend {
+ public:
+  virtual ~Backend() = default;
+  virtual const char* name() const = 0;
+  virtual std::vector<Tensor> eval_many(const Graph& g, const std::vector<NodeId>& ids, const Feeds& feeds) = 0;
+  Tensor eval_with(const Graph& g, NodeId id, const Feeds& feeds) { return eval_many(g, {id}, feeds)[0]; }
+};
+
+}  // namespace ku

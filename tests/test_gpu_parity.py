@@ -1,0 +1,304 @@
+"""Device-vs-oracle parity of the five hot-path configs and the primitives under them.
+
+Bars: integer, bool and index outputs bit-exact; f32 <= 1e-5 relative;
+bf16/f16 <= 1e-2 relative; fp8 GEMM <= 3e-2 relative against the dequantised-f64 product.
+Floating tolerances are normwise (max|err| / max|ref|) plus an elementwise bound with an
+absolute floor of the same relative size, so cancellation near zero does not hide as noise.
+Mirrors the reference's `*_matches_cpu` device tests (kurumi_metal/src/tests/*.rs).
+"""
+import numpy as np
+import pytest
+
+from kurumi_amd import DType, Graph, Tensor
+from kutest import (assert_close, bf16_bits_to_f32, f32_to_bf16_bits, interpret, rand_range, randn, rel_err,
+                    to_f32)
+
+pytestmark = pytest.mark.gpu
+
+
+def bf16_tensor(x: np.ndarray) -> Tensor:
+    return Tensor(DType.BF16, x.shape, f32_to_bf16_bits(x).tobytes())
+
+
+# ---------------- config 1: fused elementwise + reduce ----------------
+
+def cfg1_graph(n: int, m: int):
+    g = Graph()
+    x = g.input([n, m], DType.F32)
+    b = g.input([m], DType.F32)
+    xx = g.mul(x, x)
+    s = g.add(xx, g.broadcast_to(b, [n, m]))
+    r = g.relu(s)
+    h = g.mul(r, g.scalar(r, 0.5))
+    return g, x, b, g.sum(h, 1)
+
+
+@pytest.mark.parametrize("n,m", [(64, 4096), (4096, 4096), (3, 100), (1, 7)])
+def test_cfg1_fused_reduce_matches_oracle(hip, n, m):
+    print(f"cfg1 n={n} m={m}", flush=True)
+    g, x, b, y = cfg1_graph(n, m)
+    xv = rand_range([n, m], 11, -1.0, 1.0)
+    bv = rand_range([m], 12, -1.0, 1.0)
+    feeds = {x: Tensor.from_numpy(xv), b: Tensor.from_numpy(bv)}
+    got = hip.eval_with(g, y, feeds).numpy()
+    want = interpret(g, [y], feeds)[0].numpy()
+    # f64 truth of the same f32 elementwise values
+    h = np.maximum(xv * xv + bv[None, :], np.float32(0)) * np.float32(0.5)
+    truth = h.astype(np.float64).sum(axis=1)
+    assert rel_err(got, truth) <= 1e-5
+    assert_close(got, truth, rtol=1e-5, atol=1e-5 * np.abs(truth).max(), what="cfg1 vs f64")
+    assert_close(got, want, rtol=2e-5, atol=2e-5 * np.abs(want).max(), what="cfg1 vs oracle")
+
+
+def test_cfg1_is_one_kernel(hip):
+    g, x, b, y = cfg1_graph(128, 256)
+    feeds = {x: Tensor.from_numpy(np.ones((128, 256), np.float32)), b: Tensor.from_numpy(np.ones(256, np.float32))}
+    plan = hip.plan(g, [y], feeds)
+    assert len(plan.steps()) == 1, plan.steps()
+    plan.launch()
+    np.testing.assert_array_equal(plan.output(0).numpy(), np.full(128, 256.0, np.float32))
+
+
+# ---------------- config 2: softmax + argmax ----------------
+
+def softmax_graph(rows: int, cols: int, dt: DType, decomposed: bool):
+    g = Graph()
+    x = g.input([rows, cols], dt)
+    if decomposed:
+        m = g.reduce_max(x, 1)
+        mb = g.expand(g.reshape(m, [rows, 1]), [rows, cols])
+        e = g.exp(g.sub(x, mb))
+        s = g.sum(e, 1)
+        y = g.div(e, g.expand(g.reshape(s, [rows, 1]), [rows, cols]))
+    else:
+        y = g.softmax(x, 1)
+    a = g.cast(g.argmax(y, 1), DType.I32)
+    return g, x, y, a
+
+
+@pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
+@pytest.mark.parametrize("decomposed", [False, True])
+@pytest.mark.parametrize("rows,cols", [(64, 32000), (33, 1000), (5, 7)])
+def test_cfg2_softmax_argmax_matches_oracle(hip, dt, decomposed, rows, cols):
+    print(f"cfg2 {dt.name} decomposed={decomposed} {rows}x{cols}", flush=True)
+    g, x, y, a = softmax_graph(rows, cols, dt, decomposed)
+    xv = randn([rows, cols], 21, 3.0)
+    t = Tensor.from_numpy(xv) if dt == DType.F32 else bf16_tensor(xv)
+    feeds = {x: t}
+    gy, ga = hip.eval_many_with(g, [y, a], feeds)
+    wy, wa = interpret(g, [y, a], feeds)
+    # argmax is bit-exact (first index wins ties)
+    np.testing.assert_array_equal(ga.numpy(), wa.numpy())
+    assert ga.dtype == DType.I32
+    if dt == DType.F32:
+        assert_close(to_f32(gy), to_f32(wy), rtol=1e-5, atol=1e-30, what="softmax f32")
+    else:
+        assert_close(to_f32(gy), to_f32(wy), rtol=1e-2, atol=1e-2 * to_f32(wy).max(), what="softmax bf16")
+
+
+def test_cfg2_is_one_kernel(hip):
+    for decomposed in (False, True):
+        g, x, y, a = softmax_graph(16, 512, DType.BF16, decomposed)
+        plan = hip.plan(g, [y, a], {x: bf16_tensor(np.zeros((16, 512), np.float32))})
+        assert len(plan.steps()) == 1, plan.steps()
+
+
+def test_argmax_ties_and_nan_bit_exact(hip):
+    # known answer (kurumi_metal/src/tests/device_ops.rs:101-121) plus the tie / NaN rules
+    g = Graph()
+    x = g.input([6, 4], DType.F32)
+    am = g.argmax(x, 1)
+    xv = np.array([[3, 1, 4, 1], [5, 9, 2, 6], [1, 1, 1, 1], [np.nan, 5, 7, 1], [2, np.nan, 7, 7],
+                   [-np.inf, -np.inf, -np.inf, -np.inf]], np.float32)
+    feeds = {x: Tensor.from_numpy(xv)}
+    got = hip.eval_with(g, am, feeds).numpy()
+    want = interpret(g, [am], feeds)[0].numpy()
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal(got[:2], [2, 1])
+    np.testing.assert_array_equal(got[2:], [0, 0, 2, 0])
+
+
+# ---------------- config 3: GEMM ----------------
+
+@pytest.mark.parametrize("m,k,n", [(128, 256, 192), (64, 4096, 11008 // 8), (17, 33, 65)])
+def test_cfg3_bf16_gemm_matches_oracle(hip, m, k, n):
+    print(f"cfg3 {m}x{k}x{n}", flush=True)
+    g = Graph()
+    a = g.input([m, k], DType.BF16)
+    b = g.input([k, n], DType.BF16)
+    c = g.matmul(a, b)
+    av = randn([m, k], 31, 1.0 / 64)
+    bv = randn([k, n], 32, 1.0 / 64)
+    feeds = {a: bf16_tensor(av), b: bf16_tensor(bv)}
+    got = to_f32(hip.eval_with(g, c, feeds))
+    want = to_f32(interpret(g, [c], feeds)[0])
+    truth = bf16_bits_to_f32(f32_to_bf16_bits(av)).astype(np.float64) @ bf16_bits_to_f32(
+        f32_to_bf16_bits(bv)).astype(np.float64)
+    assert rel_err(got, truth) <= 1e-2
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="gemm vs oracle")
+
+
+def test_cfg3_batched_gemm_matches_oracle(hip):
+    g = Graph()
+    a = g.input([4, 256, 128], DType.BF16)
+    b = g.input([4, 128, 192], DType.BF16)
+    c = g.dot_general(a, b, [2], [1], [0], [0])
+    av = randn([4, 256, 128], 33, 1.0 / np.sqrt(128))
+    bv = randn([4, 128, 192], 34, 1.0 / np.sqrt(128))
+    feeds = {a: bf16_tensor(av), b: bf16_tensor(bv)}
+    got = to_f32(hip.eval_with(g, c, feeds))
+    want = to_f32(interpret(g, [c], feeds)[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="batched gemm")
+
+
+# ---------------- config 4: causal attention ----------------
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("b,h,s,d", [(1, 2, 128, 128), (2, 2, 80, 64)])
+def test_cfg4_attention_matches_oracle(hip, fused, b, h, s, d):
+    print(f"cfg4 fused={fused} {b},{h},{s},{d}", flush=True)
+    g = Graph()
+    q = g.input([b, h, s, d], DType.BF16)
+    k = g.input([b, h, s, d], DType.BF16)
+    v = g.input([b, h, s, d], DType.BF16)
+    o = g.sdpa_fused(q, k, v, True) if fused else g.sdpa_decomposed(q, k, v, True)
+    feeds = {q: bf16_tensor(randn([b, h, s, d], 41)), k: bf16_tensor(randn([b, h, s, d], 42)),
+             v: bf16_tensor(randn([b, h, s, d], 43))}
+    got = to_f32(hip.eval_with(g, o, feeds))
+    want = to_f32(interpret(g, [o], feeds)[0])
+    assert rel_err(got, want) <= 1e-2
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="attention")
+
+
+def test_attention_first_query_sees_first_key(hip):
+    # tests/ops.rs:256-271: causal query 0 attends only to key 0 -> out[0] == v[0]
+    s, dh = 64, 64
+    g = Graph()
+    q = g.input([1, s, dh], DType.BF16)
+    k = g.input([1, s, dh], DType.BF16)
+    v = g.input([1, s, dh], DType.BF16)
+    o = g.sdpa_fused(q, k, v, True)
+    vv = randn([1, s, dh], 44)
+    feeds = {q: bf16_tensor(randn([1, s, dh], 45)), k: bf16_tensor(randn([1, s, dh], 46)), v: bf16_tensor(vv)}
+    got = to_f32(hip.eval_with(g, o, feeds))
+    np.testing.assert_array_equal(got[0, 0], bf16_bits_to_f32(f32_to_bf16_bits(vv[0, 0])))
+
+
+# ---------------- config 5: fp8 quantized linear ----------------
+
+def test_cfg5_fp8_linear_matches_dequant_f64(hip):
+    from kurumi_amd import amp_fp8
+
+    m, k, n = 128, 512, 320
+    g = Graph()
+    x = g.input([m, k], DType.BF16)
+    wv = randn([n, k], 51, 0.02)
+    w = g.constant_bytes(DType.F32, wv.astype(np.float32).tobytes(), [n, k])
+    y0 = g.dot_general(x, g.cast(w, DType.BF16), [1], [1])
+    y = amp_fp8(g, y0)
+    xv = randn([m, k], 52)
+    feeds = {x: bf16_tensor(xv)}
+    got = to_f32(hip.eval_with(g, y, feeds))
+    want = to_f32(interpret(g, [y], feeds)[0])
+    assert rel_err(got, want) <= 3e-2
+    assert_close(got, want, rtol=3e-2, atol=3e-2 * np.abs(want).max(), what="fp8 vs oracle")
+
+
+# ---------------- casts, ints, misc primitives (bit-exact) ----------------
+
+@pytest.mark.parametrize("to", [DType.BF16, DType.F16, DType.F8E4M3, DType.F8E5M2, DType.I32, DType.U8, DType.I64,
+                                DType.BOOL, DType.F64])
+def test_casts_from_f32_bit_exact(hip, to):
+    vals = np.concatenate([randn([4000], 61, 50.0), np.array(
+        [0.0, -0.0, 1.0, -1.5, 448.0, 449.0, 464.0, 500.0, 1e-9, -1e-9, 3e38, -3e38, np.inf, -np.inf,
+         2.5, 3.5, -2.5, 0.5, 65504.0, 65520.0, 1.00390625, 1.01171875, 2 ** -7, 2 ** -10, 57344.0,
+         61440.0, 300.7, -129.5, 255.5, 256.0, 4294967296.0], np.float32)])
+    g = Graph()
+    x = g.input([vals.size], DType.F32)
+    c = g.cast(x, to)
+    feeds = {x: Tensor.from_numpy(vals)}
+    got = hip.eval_with(g, c, feeds).numpy()
+    want = interpret(g, [c], feeds)[0].numpy()
+    np.testing.assert_array_equal(got, want)
+
+
+def test_integer_ops_bit_exact(hip):
+    g = Graph()
+    a = g.input([1000], DType.I32)
+    b = g.input([1000], DType.I32)
+    outs = [g.add(a, b), g.mul(a, b), g.max(a, b), g.neg(a), g.idiv(a, b), g.bit_and(a, b), g.bit_xor(a, b),
+            g.shl(a, b), g.shr(a, b), g.lt(a, b), g.eq(a, b), g.sum(g.reshape(a, [10, 100]), 1),
+            g.argmax(g.reshape(a, [10, 100]), 1), g.reduce_max(g.reshape(a, [100, 10]), 0)]
+    rng = np.random.default_rng(7)
+    av = rng.integers(-2 ** 31, 2 ** 31, 1000, dtype=np.int64).astype(np.int32)
+    bv = rng.integers(-40, 40, 1000, dtype=np.int64).astype(np.int32)
+    bv[:5] = [0, -1, 0, 31, 33]
+    av[:2] = [-2 ** 31, -2 ** 31]
+    feeds = {a: Tensor.from_numpy(av), b: Tensor.from_numpy(bv)}
+    got = hip.eval_many_with(g, outs, feeds)
+    want = interpret(g, outs, feeds)
+    for i, (x, y) in enumerate(zip(got, want)):
+        np.testing.assert_array_equal(x.numpy(), y.numpy(), err_msg=f"output {i}")
+
+
+def test_movement_views_match_oracle(hip):
+    g = Graph()
+    x = g.input([4, 6, 5], DType.F32)
+    p = g.permute(x, [2, 0, 1])
+    s = g.slice_step(p, [(1, 5, 2), (0, 4, 1), (1, 6, 2)])
+    f = g.flip(s, [1])
+    pd = g.pad(f, [(1, 0), (0, 2), (1, 1)])
+    y = g.add(g.exp(pd), g.scalar(pd, 1.0))
+    r = g.sum(g.permute(x, [1, 0, 2]), 0)
+    outs = [p, s, f, pd, y, r]
+    xv = randn([4, 6, 5], 71)
+    feeds = {x: Tensor.from_numpy(xv)}
+    got = hip.eval_many_with(g, outs, feeds)
+    want = interpret(g, outs, feeds)
+    for i in range(4):
+        np.testing.assert_array_equal(got[i].numpy(), want[i].numpy(), err_msg=f"view {i}")
+    assert_close(got[4].numpy(), want[4].numpy(), rtol=1e-6, atol=0, what="exp(pad)")
+    assert_close(got[5].numpy(), want[5].numpy(), rtol=1e-5, atol=1e-6, what="sum axis 0 of permute")
+
+
+def test_rand_and_iota_on_device(hip):
+    g = Graph()
+    u = g.rand_uniform([3, 1000], 1234)
+    i = g.iota([4, 5], 1, DType.I32)
+    got = hip.eval_many_with(g, [u, i], {})
+    want = interpret(g, [u, i])
+    np.testing.assert_array_equal(got[0].numpy(), want[0].numpy())
+    np.testing.assert_array_equal(got[1].numpy(), want[1].numpy())
+
+
+def test_rmsnorm_and_column_reductions(hip):
+    g = Graph()
+    x = g.input([37, 300], DType.F32)
+    r = g.rmsnorm(x, 1, 1e-6)
+    c = g.sum(x, 0)
+    mx = g.reduce_max(x, 0)
+    xv = randn([37, 300], 81)
+    feeds = {x: Tensor.from_numpy(xv)}
+    got = hip.eval_many_with(g, [r, c, mx], feeds)
+    want = interpret(g, [r, c, mx], feeds)
+    assert_close(got[0].numpy(), want[0].numpy(), rtol=1e-5, atol=1e-6, what="rmsnorm")
+    assert_close(got[1].numpy(), want[1].numpy(), rtol=1e-5, atol=1e-5, what="col sum")
+    np.testing.assert_array_equal(got[2].numpy(), want[2].numpy())
+
+
+def test_eval_many_matches_single_eval(hip):
+    # backend.rs contract: eval_many shares one pass and equals per-node eval
+    g, x, y, a = softmax_graph(16, 1000, DType.F32, True)
+    feeds = {x: Tensor.from_numpy(randn([16, 1000], 91, 3.0))}
+    both = hip.eval_many_with(g, [y, a], feeds)
+    np.testing.assert_array_equal(both[1].numpy(), hip.eval_with(g, a, feeds).numpy())
+
+
+def test_missing_feed_is_an_error(hip):
+    import kurumi_amd as K
+
+    g = Graph()
+    x = g.input([4], DType.F32)
+    y = g.add(x, x)
+    with pytest.raises(K.KuError, match="missing feed"):
+        hip.eval_with(g, y, {})
