@@ -17,17 +17,15 @@ namespace {
 
 constexpr int TM = 64, TN = 64, TK = 16;
 
-template <class TI>
-struct Acc { using T = float; };
-template <> struct Acc<double> { using T = double; };
-template <> struct Acc<int8_t> { using T = uint64_t; };
-template <> struct Acc<int16_t> { using T = uint64_t; };
-template <> struct Acc<int32_t> { using T = uint64_t; };
-template <> struct Acc<int64_t> { using T = uint64_t; };
-template <> struct Acc<uint8_t> { using T = uint64_t; };
-template <> struct Acc<uint16_t> { using T = uint64_t; };
-template <> struct Acc<uint32_t> { using T = uint64_t; };
-template <> struct Acc<uint64_t> { using T = uint64_t; };
+// accumulation type by dtype tag (not by storage type: bf16/f16 are stored as uint16_t)
+template <int DT>
+struct Acc { using T = uint64_t; };  // integers wrap in 64 bits, truncated at the store
+template <> struct Acc<GT_BF16> { using T = float; };
+template <> struct Acc<GT_F16> { using T = float; };
+template <> struct Acc<GT_F8E4M3> { using T = float; };
+template <> struct Acc<GT_F8E5M2> { using T = float; };
+template <> struct Acc<GT_F32> { using T = float; };
+template <> struct Acc<GT_F64> { using T = double; };
 
 template <int DT, int OT, class TI, class TO, class TA>
 __global__ void __launch_bounds__(256) gemm_generic_k(GemmArgs a) {
@@ -90,7 +88,7 @@ __global__ void __launch_bounds__(256) gemm_generic_k(GemmArgs a) {
 
 template <int DT, class TI, int OT, class TO>
 void launch_t(const GemmArgs& a, hipStream_t s) {
-  using TA = typename Acc<TI>::T;
+  using TA = typename Acc<DT>::T;
   dim3 grid((unsigned)((a.n + TN - 1) / TN), (unsigned)((a.m + TM - 1) / TM), (unsigned)a.batch);
   hipLaunchKernelGGL((gemm_generic_k<DT, OT, TI, TO, TA>), grid, dim3(256), 0, s, a);
 }

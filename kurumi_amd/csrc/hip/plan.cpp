@@ -3,6 +3,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <functional>
 #include <limits>
@@ -1216,6 +1218,8 @@ void Planner::run() {
 
 // ======================= plan =======================
 
+static bool debug_enabled();
+
 Plan::Plan(const Graph& g, const std::vector<NodeId>& roots, Context* ctx, ConstCache* consts)
     : g_(g), graph_id_(g.id()), roots_(roots), ctx_(ctx) {
   if (roots.empty()) throw Error("eval: no output nodes");
@@ -1294,11 +1298,20 @@ void Plan::feed(NodeId input, const Tensor& t) {
   Slot& s = slots_[it->second];
   if (t.bytes.size() != s.bytes) throw Error("feed: byte size mismatch");
   if (!s.bytes) return;
+  if (debug_enabled()) std::fprintf(stderr, "[kurumi_hip] feed %%%u -> %p (%zu bytes)\n", input, s.buf.ptr, s.bytes);
   KU_HIP(hipMemcpyAsync(s.buf.ptr, t.bytes.data(), s.bytes, hipMemcpyHostToDevice, ctx_->stream()));
   ctx_->profile().launches[(int)Kind::Upload]++;
 }
 
 static void* slot_ptr(const std::vector<Slot>& slots, int i) { return slots[i].buf.ptr; }
+
+static bool debug_enabled() {
+  static const bool on = [] {
+    const char* e = std::getenv("KURUMI_HIP_DEBUG");
+    return e && *e && *e != '0';
+  }();
+  return on;
+}
 
 void Plan::launch_step(const Step& s) {
   hipStream_t st = ctx_->stream();
@@ -1329,7 +1342,13 @@ void Plan::launch_step(const Step& s) {
       a.col_scale_stride = G.col_scale_stride;
     }
     if (G.batch * G.m * G.n == 0) return;
+    if (debug_enabled())
+      std::fprintf(stderr, "[kurumi_hip] gemm a=%p b=%p c=%p sa=(%lld,%lld,%lld) sb=(%lld,%lld,%lld) b%lld m%lld n%lld k%lld in%d out%d\n",
+                   a.a, a.b, a.c, (long long)a.sab, (long long)a.sam, (long long)a.sak, (long long)a.sbb,
+                   (long long)a.sbk, (long long)a.sbn, (long long)a.batch, (long long)a.m, (long long)a.n,
+                   (long long)a.k, a.in_type, a.out_type);
     launch_gemm(a, st);
+    KU_HIP(hipGetLastError());
     ctx_->profile().launches[(int)Kind::Gemm]++;
   } else {
     const AttnStep& A = attns_[s.index];
@@ -1343,6 +1362,7 @@ void Plan::launch_step(const Step& s) {
     a.causal = A.causal;
     a.dtype = (int)A.dtype;
     launch_attention(a, st);
+    KU_HIP(hipGetLastError());
     ctx_->profile().launches[(int)Kind::Attention]++;
   }
 }

@@ -91,7 +91,14 @@ def test_cfg2_softmax_argmax_matches_oracle(hip, dt, decomposed, rows, cols):
     np.testing.assert_array_equal(ga.numpy(), wa.numpy())
     assert ga.dtype == DType.I32
     if dt == DType.F32:
-        assert_close(to_f32(gy), to_f32(wy), rtol=1e-5, atol=1e-30, what="softmax f32")
+        # The oracle folds the 32000-term row sum sequentially in f32 (interp/nn.rs:53-58), which
+        # alone carries ~1e-5..1e-4 relative error; the 1e-5 bar is therefore taken against the
+        # f64 softmax of the same inputs, and the oracle difference is bounded at 1e-4.
+        x64 = xv.astype(np.float64)
+        e = np.exp(x64 - x64.max(axis=1, keepdims=True))
+        truth = e / e.sum(axis=1, keepdims=True)
+        assert_close(to_f32(gy), truth, rtol=1e-5, atol=1e-30, what="softmax f32 vs f64")
+        assert_close(to_f32(gy), to_f32(wy), rtol=1e-4, atol=1e-30, what="softmax f32 vs oracle")
     else:
         assert_close(to_f32(gy), to_f32(wy), rtol=1e-2, atol=1e-2 * to_f32(wy).max(), what="softmax bf16")
 
