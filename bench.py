@@ -1,0 +1,309 @@
+"""kurumi_hip benchmark: the five BASELINE configs on one MI355X, plus the CPU baseline.
+
+The headline line (metric/value) is config 2 — row softmax over [8192, 32000] f32 built from
+primitives (reduce_max, sub, exp, sum, div) followed by argmax -> int32 — as HBM GB/s of the
+single fused kernel's algorithmic traffic. Every config runs as a device-resident plan
+(inputs uploaded once, threefry-seeded synthetic data generated on the device), W untimed
+launches, then K timed launches bracketed by stream synchronisation. Per-kernel durations
+come from hipEvents recorded on the plan's own stream. The other configs are reported under
+"configs" with their own roofline fractions.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+FP8_PEAK_TFLOPS = 5033.2
+
+
+def _ku():
+    import kurumi_amd as K
+
+    return K
+
+
+def device_values(hip, build, shape, seed, dtype):
+    """Generate kurumi's seeded random tensor on the device (threefry2x32 inside the graph)."""
+    K = _ku()
+    g = K.Graph()
+    x = build(g, list(shape), seed)
+    if dtype != K.DType.F32:
+        x = g.cast(x, dtype)
+    return hip.eval(g, x)
+
+
+def scaled_randn(std):
+    return lambda g, s, sd: g.mul(g.randn(s, sd), g.expand(g.constant(np.array([std], np.float32).reshape(
+        [1] * len(s))), s))
+
+
+def time_plan(plan, steps: int, warmup: int, use_graph: bool = False):
+    for _ in range(warmup):
+        plan.launch(use_graph)
+    plan.sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        plan.launch(use_graph)
+    plan.sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+    per_step = plan.time_steps(max(steps, 5))
+    return wall_ms, per_step, plan.steps()
+
+
+def roofline_hbm(bytes_per_launch: float, kernel_ms: float):
+    gbs = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+
+
+def roofline_mfma(flops: float, kernel_ms: float, peak_tflops: float):
+    tf = flops / (kernel_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": peak_tflops, "unit": "TFLOP/s",
+            "frac": round(tf / peak_tflops, 4), "traffic": None}
+
+
+# ---------------- config 2 (headline) ----------------
+
+def softmax_graph(K, rows, cols, dt):
+    g = K.Graph()
+    x = g.input([rows, cols], dt)
+    m = g.reduce_max(x, 1)
+    e = g.exp(g.sub(x, g.expand(g.reshape(m, [rows, 1]), [rows, cols])))
+    s = g.sum(e, 1)
+    y = g.div(e, g.expand(g.reshape(s, [rows, 1]), [rows, cols]))
+    a = g.cast(g.argmax(y, 1), K.DType.I32)
+    return g, x, y, a
+
+
+def bench_cfg2(hip, steps, warmup, dt_name="f32"):
+    K = _ku()
+    rows, cols = 8192, 32000
+    dt = K.DType.F32 if dt_name == "f32" else K.DType.BF16
+    xt = device_values(hip, scaled_randn(3.0), [rows, cols], 2024, dt)
+    g, x, y, a = softmax_graph(K, rows, cols, dt)
+    plan = hip.plan(g, [y, a], {x: xt})
+    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    w = 4 if dt == K.DType.F32 else 2
+    algo_bytes = rows * cols * w * 2 + rows * 4  # read x, write y, write int32 argmax
+    kms = max(per_step)
+    k = per_step.index(kms)
+    return {
+        "workload": f"softmax+argmax [{rows},{cols}] {dt_name} (decomposed primitives)",
+        "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "dominant": labels[k],
+        "algo_bytes": algo_bytes, "value_gbs": algo_bytes / (wall_ms * 1e-3) / 1e9,
+        "roofline": roofline_hbm(algo_bytes, kms),
+        "_graph": (g, x, y, a, xt),
+    }
+
+
+def cpu_baseline_cfg2(xt_full, rows_sample=256, cols=32000):
+    """The oracle (single-threaded C++ restatement of kurumi's interpreter) on a row sample."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import kutest
+    K = _ku()
+    x_all = xt_full.numpy()
+    xs = np.ascontiguousarray(x_all[:rows_sample])
+    g, x, y, a = softmax_graph(K, rows_sample, cols, K.DType.F32)
+    feeds = {x: K.Tensor.from_numpy(xs)}
+    kutest.interpret(g, [y, a], feeds)  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        kutest.interpret(g, [y, a], feeds)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > 8.0 or reps >= 20:
+            break
+    sec = el / reps
+    algo_bytes = rows_sample * cols * 8 + rows_sample * 4
+    return {"value": round(algo_bytes / sec / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{rows_sample} of 8192 rows x 32000 f32, decomposed softmax + argmax via the oracle "
+                      f"interpreter, {reps} reps, {sec * 1e3:.1f} ms/rep, host nproc={os.cpu_count()}"}
+
+
+# ---------------- other configs ----------------
+
+def bench_cfg1(hip, steps, warmup):
+    K = _ku()
+    n = 4096
+    plans = []
+    # rotate 5 input sets (5 x 64 MiB > 256 MiB MALL) so the kernel streams from HBM
+    for r in range(5):
+        g = K.Graph()
+        x = g.input([n, n], K.DType.F32)
+        b = g.input([n], K.DType.F32)
+        h = g.mul(g.relu(g.add(g.mul(x, x), g.broadcast_to(b, [n, n]))), g.scalar(x, 0.5))
+        y = g.sum(h, 1)
+        xt = device_values(hip, lambda gg, s, sd: gg.rand_range(s, sd, -1.0, 1.0), [n, n], 100 + r, K.DType.F32)
+        bt = device_values(hip, lambda gg, s, sd: gg.rand_range(s, sd, -1.0, 1.0), [n], 200 + r, K.DType.F32)
+        plans.append((hip.plan(g, [y], {x: xt, b: bt}), g))
+    for _ in range(warmup):
+        for p, _g in plans:
+            p.launch()
+    plans[0][0].sync()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for p, _g in plans:
+            p.launch()
+    plans[0][0].sync()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / (steps * len(plans))
+    algo_bytes = 4 * n * n + 4 * n + 4 * n
+    return {"workload": "sum_lastaxis(relu(x*x+b)*0.5) [4096,4096] f32, 5 rotating input sets",
+            "ms_per_step": wall_ms, "kernels": plans[0][0].steps(), "algo_bytes": algo_bytes,
+            "roofline": roofline_hbm(algo_bytes, wall_ms)}
+
+
+def bench_gemm(hip, steps, warmup, batched=False):
+    K = _ku()
+    g = K.Graph()
+    if batched:
+        sa, sb, std = [8, 2048, 128], [8, 128, 2048], 1.0 / np.sqrt(128)
+        a = g.input(sa, K.DType.BF16)
+        b = g.input(sb, K.DType.BF16)
+        c = g.dot_general(a, b, [2], [1], [0], [0])
+        flops = 2 * 8 * 2048 * 2048 * 128
+    else:
+        sa, sb, std = [4096, 4096], [4096, 11008], 1.0 / 64
+        a = g.input(sa, K.DType.BF16)
+        b = g.input(sb, K.DType.BF16)
+        c = g.matmul(a, b)
+        flops = 2 * 4096 * 4096 * 11008
+    at = device_values(hip, scaled_randn(std), sa, 301, K.DType.BF16)
+    bt = device_values(hip, scaled_randn(std), sb, 302, K.DType.BF16)
+    plan = hip.plan(g, [c], {a: at, b: bt})
+    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    kms = next(t for t, l in zip(per_step, labels) if l.startswith("gemm"))
+    out = {"workload": ("batched [8,2048,128]@[8,128,2048]" if batched else "[4096,4096]@[4096,11008]") + " bf16",
+           "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "flops": flops,
+           "roofline": roofline_mfma(flops, kms, BF16_PEAK_TFLOPS)}
+    if batched:
+        byts = 2 * (8 * 2048 * 128 * 2) + 8 * 2048 * 2048 * 2
+        out["roofline_hbm"] = roofline_hbm(byts, kms)
+    return out
+
+
+def bench_attention(hip, steps, warmup):
+    K = _ku()
+    B, H, S, D = 4, 32, 2048, 128
+    g = K.Graph()
+    q = g.input([B, H, S, D], K.DType.BF16)
+    k = g.input([B, H, S, D], K.DType.BF16)
+    v = g.input([B, H, S, D], K.DType.BF16)
+    o = g.sdpa(q, k, v, True)
+    feeds = {n: device_values(hip, lambda gg, s, sd: gg.randn(s, sd), [B, H, S, D], 400 + i, K.DType.BF16)
+             for i, n in enumerate([q, k, v])}
+    plan = hip.plan(g, [o], feeds)
+    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    flops = 4 * B * H * S * S * D // 2
+    return {"workload": "causal sdpa B4 H32 S2048 D128 bf16 (Op::Sdpa via g.sdpa)", "ms_per_step": wall_ms,
+            "kernels": labels, "kernel_ms": per_step, "flops": flops,
+            "roofline": roofline_mfma(flops, max(per_step), BF16_PEAK_TFLOPS)}
+
+
+def bench_fp8(hip, steps, warmup):
+    K = _ku()
+    M, Kd, N = 2048, 4096, 11008
+    wt = device_values(hip, scaled_randn(0.02), [N, Kd], 501, K.DType.F32)
+    g = K.Graph()
+    x = g.input([M, Kd], K.DType.BF16)
+    w = g.constant_bytes(K.DType.F32, wt.data, [N, Kd])
+    y0 = g.dot_general(x, g.cast(w, K.DType.BF16), [1], [1])
+    y = K.amp_fp8(g, y0)
+    xt = device_values(hip, lambda gg, s, sd: gg.randn(s, sd), [M, Kd], 502, K.DType.BF16)
+    plan = hip.plan(g, [y], {x: xt})
+    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    flops = 2 * M * N * Kd
+    gemm_ms = next(t for t, l in zip(per_step, labels) if l.startswith("gemm"))
+    return {"workload": "e4m3 linear X[2048,4096] W[11008,4096]^T per-row/per-tensor scales, bf16 out",
+            "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "flops": flops,
+            "roofline": roofline_mfma(flops, gemm_ms, FP8_PEAK_TFLOPS)}
+
+
+def bench_copy(hip, steps, warmup):
+    """A plain streaming copy of 2^28 f32 (1 GiB read + 1 GiB write) through a one-leaf region."""
+    K = _ku()
+    n = 1 << 28
+    g = K.Graph()
+    x = g.input([n // 4096, 4096], K.DType.F32)
+    y = g.neg(g.neg(x))
+    xt = device_values(hip, lambda gg, s, sd: gg.rand_uniform(s, sd), [n // 4096, 4096], 7, K.DType.F32)
+    plan = hip.plan(g, [y], {x: xt})
+    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    return {"workload": "copy 1 GiB f32 (y = -(-x))", "kernels": labels, "kernel_ms": per_step,
+            "algo_bytes": 2 * 4 * n, "roofline": roofline_hbm(2 * 4 * n, max(per_step))}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe-copy", action="store_true",
+                    help="also run a plain 1 GiB f32 copy kernel (counter calibration / copy ceiling)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"kurumi_hip bench: this run measures one GPU only; --gpus {args.gpus} is not supported "
+              "(every config shards with no exchange step; see DESIGN.md)", file=sys.stderr)
+        return 2
+    K = _ku()
+    hip = K.HipBackend()
+    cfgs = {c.strip() for c in args.configs.split(",") if c.strip()}
+    head = bench_cfg2(hip, args.steps, args.warmup, "f32")
+    g, x, y, a, xt = head.pop("_graph")
+    extra = {}
+    if "2" in cfgs:
+        b16 = bench_cfg2(hip, args.steps, args.warmup, "bf16")
+        b16.pop("_graph")
+        extra["cfg2_bf16"] = b16
+    if "1" in cfgs:
+        extra["cfg1"] = bench_cfg1(hip, args.steps, args.warmup)
+    if "3" in cfgs:
+        extra["cfg3"] = bench_gemm(hip, max(3, args.steps // 4), 1)
+        extra["cfg3b"] = bench_gemm(hip, args.steps, args.warmup, batched=True)
+    if "4" in cfgs:
+        extra["cfg4"] = bench_attention(hip, max(3, args.steps // 4), 1)
+    if "5" in cfgs:
+        extra["cfg5"] = bench_fp8(hip, max(3, args.steps // 4), 1)
+    if args.probe_copy:
+        extra["copy_probe"] = bench_copy(hip, args.steps, args.warmup)
+    cpu = None if args.no_cpu else cpu_baseline_cfg2(xt)
+    line = {
+        "metric": "fused softmax+argmax HBM GB/s (cfg 2, f32 [8192,32000]); GEMM/attn TFLOP/s under configs",
+        "value": round(head["value_gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: threefry2x32-seeded N(0, 3^2) logits generated on the device",
+        "config": {"workload": head["workload"], "rows": 8192, "cols": 32000, "outputs": "softmax f32 + argmax i32",
+                   "kernels": head["kernels"], "algo_bytes_per_step": head["algo_bytes"]},
+        "roofline": head["roofline"],
+        "cpu_baseline": cpu,
+        "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
+                    for k, v in extra.items()},
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

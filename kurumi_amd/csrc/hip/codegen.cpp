@@ -14,6 +14,7 @@
 // kurumi_metal/src/backend/fuse/emit.rs:80-142.
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <functional>
 #include <map>
 #include <set>
@@ -199,6 +200,17 @@ struct Gen {
   void emit_red_finish(int ni, int phase);
   std::string leaf_base(int leaf) const;
   std::string generate(RegionCode* rc);
+  std::string finish(const std::string& prefix, RegionCode* rc) {
+    std::string src = o.str();
+    uint64_t h = 1469598103934665603ull;
+    for (unsigned char ch : src) h = (h ^ ch) * 1099511628211ull;
+    char hex[16];
+    std::snprintf(hex, sizeof hex, "%06llx", (unsigned long long)(h & 0xffffff));
+    rc->entry = prefix + "_" + hex;
+    size_t at = src.find("KU_ENTRY_PLACEHOLDER");
+    src.replace(at, std::string("KU_ENTRY_PLACEHOLDER").size(), rc->entry);
+    return src;
+  }
 };
 
 std::string Gen::op_expr(int ni, const std::string& j) const {
@@ -366,13 +378,42 @@ void Gen::schedule() {
     if (is_red(n.kind)) red_inputs.insert(n.in[0]);
   unroll = !flat && NC <= 16;
   if (!flat && NC <= 16) {
-    int regs = 0;
+    // Greedy register budget: values feeding later reductions first (latest level first),
+    // then leaves; a candidate only counts while some later phase still has to recompute it.
     std::vector<int> cand;
     for (auto& kv : uses)
       if (kv.second >= 2 && (node(kv.first).kind == RK_LEAF || red_inputs.count(kv.first))) cand.push_back(kv.first);
-    for (int c : cand) regs += NC * V * (node(c).dtype == DType::F64 || dt_width(node(c).dtype) == 8 ? 2 : 1);
-    if (regs <= 160)
-      for (int c : cand) cached.insert(c);
+    std::sort(cand.begin(), cand.end(), [&](int x, int y) {
+      bool rx = red_inputs.count(x), ry = red_inputs.count(y);
+      if (rx != ry) return rx;
+      return node(x).level > node(y).level;
+    });
+    int regs = 0;
+    for (int c : cand) {
+      int cost = NC * V * (node(c).dtype == DType::F64 || dt_width(node(c).dtype) == 8 ? 2 : 1);
+      // skip a leaf whose every later use already reads a cached descendant
+      bool still_needed = true;
+      if (node(c).kind == RK_LEAF) {
+        std::vector<std::set<int>> trial(nph + 2);
+        std::function<void(int, int)> walk = [&](int p, int n) {
+          if (!full(n) || trial[p].count(n)) return;
+          trial[p].insert(n);
+          if (cached.count(n) && first_phase[n] < p) return;
+          for (int i : node(n).in) walk(p, i);
+        };
+        for (size_t i = 0; i < R.nodes.size(); ++i) {
+          if (is_red(R.nodes[i].kind)) walk(R.nodes[i].level, R.nodes[i].in[0]);
+          if (store_phase[i]) walk(store_phase[i], (int)i);
+        }
+        int phases = 0;
+        for (int p = 1; p <= nph; ++p) phases += trial[p].count(c) ? 1 : 0;
+        still_needed = phases >= 2;
+      }
+      if (still_needed && regs + cost <= 160) {
+        cached.insert(c);
+        regs += cost;
+      }
+    }
   }
   // with caches, later phases need fewer recomputations: rebuild need sets
   if (!cached.empty()) {
@@ -623,8 +664,12 @@ std::string Gen::generate(RegionCode* rc) {
   plan_layout();
   schedule();
   std::ostringstream nm;
-  nm << "ku_" << (flat ? "ew" : "line") << index;
-  std::string entry = nm.str();
+  // placeholder entry; the final name carries the iteration shape and a hash of the body so
+  // that profiles can tell kernels apart (one name per distinct generated kernel)
+  nm << "ku_" << (flat ? "ew" : "line");
+  for (size_t d = 0; d < R.S.size(); ++d) nm << (d ? "x" : "_") << R.S[d];
+  std::string entry = "KU_ENTRY_PLACEHOLDER";
+  std::string prefix = nm.str();
   for (auto& l : R.leaves) param(l.slot);
   for (auto& op : R.outputs) param(op.second);
   o << kDevicePrelude;
@@ -695,9 +740,8 @@ std::string Gen::generate(RegionCode* rc) {
     o << "  }\n}\n";
     rc->grid = (unsigned)((N / (uint64_t)V + WG - 1) / WG);
     rc->block = WG;
-    rc->entry = entry;
     rc->arg_slots = param_slots;
-    return o.str();
+    return finish(prefix, rc);
   }
   // ---- line kernel ----
   // caches
@@ -758,9 +802,8 @@ std::string Gen::generate(RegionCode* rc) {
   o << "}\n";
   rc->grid = (unsigned)((lines + GPW - 1) / GPW);
   rc->block = WG;
-  rc->entry = entry;
   rc->arg_slots = param_slots;
-  return o.str();
+  return finish(prefix, rc);
 }
 
 }  // namespace

@@ -44,25 +44,45 @@ bool is_linear(const Graph& g, NodeId id) {
 
 }  // namespace
 
+// Host values of a constant weight: a float Const, or a Cast{f32|bf16|f16} of one (the cast is
+// folded with its rounding). False for anything else.
+bool const_weight_f32(const Graph& g, NodeId w, std::vector<float>* out) {
+  const Node& n = g.node(w);
+  DType round_to = DType::F32;
+  const Node* c = &n;
+  if (n.op.kind == OpKind::Cast) {
+    round_to = n.op.to;
+    if (round_to != DType::F32 && round_to != DType::BF16 && round_to != DType::F16) return false;
+    c = &g.node(n.src[0]);
+  }
+  if (c->op.kind != OpKind::Const) return false;
+  DType dt = c->op.data_dtype;
+  if (!(dt == DType::F32 || dt == DType::F64 || dt == DType::BF16 || dt == DType::F16)) return false;
+  size_t cnt = numel(c->op.shape), wd = dt_width(dt);
+  const uint8_t* p = c->op.data->data();
+  out->resize(cnt);
+  for (size_t i = 0; i < cnt; ++i) {
+    double v = load_as_f64(dt, p + i * wd);
+    if (round_to == DType::BF16) v = bf16_to_f32(f64_to_bf16(v));
+    else if (round_to == DType::F16) v = f16_to_f64(f64_to_f16(v));
+    (*out)[i] = static_cast<float>(v);
+  }
+  return true;
+}
+
 // Quantize a row-major [rows, cols] weight per row: sw[r] = max|w[r,:]| / 448 (f32),
 // wq = e4m3(w / sw[r]) with round-to-nearest-even. Rows of zeros get sw = 1.
-void quantize_rows_e4m3(const Graph& g, NodeId w, std::vector<uint8_t>* wq, std::vector<float>* sw) {
-  const Node& n = g.node(w);
-  size_t rows = n.shape[0], cols = n.shape[1];
-  size_t wd = dt_width(n.op.data_dtype);
-  const uint8_t* p = n.op.data->data();
+void quantize_rows_e4m3(const std::vector<float>& w, size_t rows, size_t cols, std::vector<uint8_t>* wq,
+                        std::vector<float>* sw) {
   wq->resize(rows * cols);
   sw->resize(rows);
   for (size_t r = 0; r < rows; ++r) {
     float mx = 0.f;
-    for (size_t c = 0; c < cols; ++c) mx = std::fmax(mx, std::fabs((float)load_as_f64(n.op.data_dtype, p + (r * cols + c) * wd)));
+    for (size_t c = 0; c < cols; ++c) mx = std::fmax(mx, std::fabs(w[r * cols + c]));
     float s = mx / 448.0f;
     if (!(s > 0.f) || !std::isfinite(s)) s = 1.0f;
     (*sw)[r] = s;
-    for (size_t c = 0; c < cols; ++c) {
-      float v = (float)load_as_f64(n.op.data_dtype, p + (r * cols + c) * wd);
-      (*wq)[r * cols + c] = f32_to_f8e4m3(v / s);
-    }
+    for (size_t c = 0; c < cols; ++c) (*wq)[r * cols + c] = f32_to_f8e4m3(w[r * cols + c] / s);
   }
 }
 
@@ -85,14 +105,11 @@ NodeId amp_fp8(Graph& g, NodeId root) {
       DType out = n.dtype;
       // weight: host quantization for constants, in-graph otherwise
       NodeId wq_node, sw_node;
-      const Node& wn = g.node(w);
-      bool host_quant = wn.op.kind == OpKind::Const &&
-                        (wn.op.data_dtype == DType::F32 || wn.op.data_dtype == DType::F64 ||
-                         wn.op.data_dtype == DType::BF16 || wn.op.data_dtype == DType::F16);
-      if (host_quant) {
+      std::vector<float> wv;
+      if (const_weight_f32(g, w, &wv)) {
         std::vector<uint8_t> wq;
         std::vector<float> sw;
-        quantize_rows_e4m3(g, w, &wq, &sw);
+        quantize_rows_e4m3(wv, N, K, &wq, &sw);
         wq_node = g.constant_bytes(DType::F8E4M3, wq.data(), wq.size(), {N, K});
         sw_node = g.constant_f32(sw, {N});
       } else {

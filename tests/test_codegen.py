@@ -1,0 +1,140 @@
+"""Fusion planning and code generation on the CPU (no GPU): every hot-path graph lowers to the
+expected number of device steps and each generated kernel compiles for gfx950 with hipRTC."""
+import numpy as np
+import pytest
+
+import kurumi_amd as K
+from kurumi_amd import DType, Graph
+
+
+def steps(src: str):
+    return [l.split(": ", 1)[1] for l in src.splitlines() if l.startswith("// step ")]
+
+
+def cfg1(n=4096):
+    g = Graph()
+    x = g.input([n, n], DType.F32)
+    b = g.input([n], DType.F32)
+    y = g.sum(g.mul(g.relu(g.add(g.mul(x, x), g.broadcast_to(b, [n, n]))), g.scalar(x, 0.5)), 1)
+    return g, [y]
+
+
+def cfg2(dt, decomposed, rows=8192, cols=32000):
+    g = Graph()
+    x = g.input([rows, cols], dt)
+    if decomposed:
+        m = g.reduce_max(x, 1)
+        e = g.exp(g.sub(x, g.expand(g.reshape(m, [rows, 1]), [rows, cols])))
+        y = g.div(e, g.expand(g.reshape(g.sum(e, 1), [rows, 1]), [rows, cols]))
+    else:
+        y = g.softmax(x, 1)
+    return g, [y, g.cast(g.argmax(y, 1), DType.I32)]
+
+
+def test_cfg1_single_line_kernel_compiles():
+    g, roots = cfg1()
+    st = steps(g.codegen(roots, compile=True))
+    assert len(st) == 1 and st[0].startswith("ku_line_4096x4096")
+
+
+@pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
+@pytest.mark.parametrize("decomposed", [True, False])
+def test_cfg2_single_kernel_for_softmax_and_argmax(dt, decomposed):
+    g, roots = cfg2(dt, decomposed)
+    src = g.codegen(roots, compile=True)
+    st = steps(src)
+    assert len(st) == 1 and st[0].startswith("ku_line_8192x32000")
+    # the line stays in registers: caches for the loaded row, one LDS fold per reduction level
+    assert "cache" in src
+
+
+def test_cfg3_gemm_steps():
+    g = Graph()
+    c = g.matmul(g.input([4096, 4096], DType.BF16), g.input([4096, 11008], DType.BF16))
+    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn b1 m4096 n11008 k4096"]
+    g = Graph()
+    c = g.dot_general(g.input([8, 2048, 128], DType.BF16), g.input([8, 128, 2048], DType.BF16), [2], [1], [0], [0])
+    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn b8 m2048 n2048 k128"]
+    g = Graph()
+    c = g.dot_general(g.input([64, 256], DType.BF16), g.input([128, 256], DType.BF16), [1], [1])
+    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nt b1 m64 n128 k256"]
+    g = Graph()  # transposed lhs is canonicalised by a copy kernel first
+    c = g.dot_general(g.input([256, 64], DType.BF16), g.input([256, 128], DType.BF16), [0], [0])
+    st = steps(g.codegen([c], compile=True))
+    assert len(st) == 2 and st[0].startswith("ku_ew") and st[1].startswith("gemm_mfma_bf16_nn")
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_cfg4_attention_is_one_step(fused):
+    g = Graph()
+    q, k, v = (g.input([4, 32, 2048, 128], DType.BF16) for _ in range(3))
+    o = g.sdpa_fused(q, k, v, True) if fused else g.sdpa_decomposed(q, k, v, True)
+    st = steps(g.codegen([o]))
+    assert len(st) == 1 and st[0].startswith("attn") and "causal" in st[0]
+
+
+def test_decomposed_attention_with_non_causal_bias_is_not_matched():
+    g = Graph()
+    s = 64
+    q, k, v = (g.input([1, 2, s, 32], DType.F32) for _ in range(3))
+    raw = g.dot_general(q, k, [3], [3], [0, 1], [0, 1])
+    sc = g.mul(raw, g.scalar(raw, 0.125))
+    bias = np.zeros((s, s), np.float32)
+    bias[0, 5] = -1.0  # not a causal mask
+    sc = g.add(sc, g.expand(g.reshape(g.constant(bias), [1, 1, s, s]), [1, 2, s, s]))
+    o = g.dot_general(g.softmax(sc, 3), v, [3], [2], [0, 1], [0, 1])
+    st = steps(g.codegen([o], compile=True))
+    assert not any(x.startswith("attn") for x in st) and len(st) == 3
+
+
+def test_cfg5_fp8_linear_lowering():
+    g = Graph()
+    x = g.input([2048, 4096], DType.BF16)
+    w = g.constant(np.random.default_rng(0).normal(0, 0.02, (256, 4096)).astype(np.float32))
+    y = K.amp_fp8(g, g.dot_general(x, g.cast(w, DType.BF16), [1], [1]))
+    assert g.dtype(y) == DType.BF16 and g.shape(y) == (2048, 256)
+    st = steps(g.codegen([y], compile=True))
+    # weights quantised on the host; on device: absmax rows, absmax, scale, quantise, fp8 GEMM
+    assert st[-1] == "gemm_mfma_e4m3_nt b1 m2048 n256 k4096"
+    assert not any("256x4096" in s for s in st)
+    assert len(st) <= 6
+
+
+def test_amp_fp8_host_quantization_matches_numpy():
+    import kutest
+
+    rng = np.random.default_rng(1)
+    wv = rng.normal(0, 0.02, (16, 64)).astype(np.float32)
+    g = Graph()
+    x = g.input([4, 64], DType.F32)
+    y = K.amp_fp8(g, g.dot_general(x, g.constant(wv), [1], [1]))
+    lines = g.dump(y).splitlines()
+    wq_id = next(int(l.split()[0][1:]) for l in lines if "Const[16, 64]" in l)
+    sw_id = next(int(l.split()[0][1:]) for l in lines if "Const[16]" in l)
+    wq = kutest.interpret(g, [wq_id])[0].numpy()
+    sw = kutest.interpret(g, [sw_id])[0].numpy()
+    np.testing.assert_array_equal(sw, (np.abs(wv).max(1) / np.float32(448)).astype(np.float32))
+    want = kutest.cast_bits((wv / sw[:, None]).astype(np.float32), DType.F32, DType.F8E4M3)
+    np.testing.assert_array_equal(wq, want)
+
+
+def test_generic_paths_compile():
+    g = Graph()
+    x = g.input([5, 6, 7], DType.F32)
+    i = g.input([5, 6, 7], DType.I16)
+    outs = [g.sum(x, 0), g.reduce_max(x, 1), g.argmax(x, 2), g.prod(g.permute(x, [2, 0, 1]), 1),
+            g.cast(g.floor(g.mul(x, g.scalar(x, 3.0))), DType.I8), g.shl(i, i), g.idiv(i, i),
+            g.bitcast(g.cast(x, DType.BF16), DType.I16), g.pad(x, [(1, 1), (0, 2), (3, 0)]),
+            g.flip(g.slice_step(x, [(0, 5, 2), (1, 6, 1), (0, 7, 3)]), [0, 2]),
+            g.where(g.lt(x, g.scalar(x, 0.0)), x, g.neg(x)), g.rmsnorm(x, 2, 1e-6), g.iota([3, 4], 0, DType.F16),
+            g.rand_uniform([2, 9], 5)]
+    src = g.codegen(outs, compile=True)
+    assert len(steps(src)) >= 5
+
+
+def test_unsupported_dtype_is_an_error_not_a_fallback():
+    g = Graph()
+    z = g.input([4], DType.C64)
+    y = g.add(z, z)
+    with pytest.raises(K.KuError, match="complex"):
+        g.codegen([y])
