@@ -63,10 +63,21 @@ def time_plan(plan, steps: int, warmup: int, use_graph: bool = False):
     return wall_ms, per_step, plan.steps()
 
 
-def roofline_hbm(bytes_per_launch: float, kernel_ms: float):
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of a generated kernel, from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (profiles/hbm_traffic.json, scaled by the copy-kernel calibration).
+    Keyed by the kernel's name, which hashes its source: a changed kernel reads as null."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists():
+        return None
+    rec = json.loads(path.read_text()).get("kernels", {}).get(kernel)
+    return rec["traffic_bytes"] if rec else None
+
+
+def roofline_hbm(bytes_per_launch: float, kernel_ms: float, kernel: str | None = None):
     gbs = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None}
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel) if kernel else None}
 
 
 def roofline_mfma(flops: float, kernel_ms: float, peak_tflops: float):
@@ -104,7 +115,7 @@ def bench_cfg2(hip, steps, warmup, dt_name="f32"):
         "workload": f"softmax+argmax [{rows},{cols}] {dt_name} (decomposed primitives)",
         "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "dominant": labels[k],
         "algo_bytes": algo_bytes, "value_gbs": algo_bytes / (wall_ms * 1e-3) / 1e9,
-        "roofline": roofline_hbm(algo_bytes, kms),
+        "roofline": roofline_hbm(algo_bytes, kms, labels[k]),
         "_graph": (g, x, y, a, xt),
     }
 
@@ -162,7 +173,7 @@ def bench_cfg1(hip, steps, warmup):
     algo_bytes = 4 * n * n + 4 * n + 4 * n
     return {"workload": "sum_lastaxis(relu(x*x+b)*0.5) [4096,4096] f32, 5 rotating input sets",
             "ms_per_step": wall_ms, "kernels": plans[0][0].steps(), "algo_bytes": algo_bytes,
-            "roofline": roofline_hbm(algo_bytes, wall_ms)}
+            "roofline": roofline_hbm(algo_bytes, wall_ms, plans[0][0].steps()[0])}
 
 
 def bench_gemm(hip, steps, warmup, batched=False):
@@ -265,6 +276,15 @@ def main() -> int:
     head = bench_cfg2(hip, args.steps, args.warmup, "f32")
     g, x, y, a, xt = head.pop("_graph")
     extra = {}
+    # the same step through the host boundary (ku_eval_many with host feeds -> host results):
+    # PCIe-inclusive rate, reported beside the device-resident value
+    hip.eval_many_with(g, [y, a], {x: xt})
+    t0 = time.perf_counter()
+    for _ in range(2):
+        hip.eval_many_with(g, [y, a], {x: xt})
+    host_ms = (time.perf_counter() - t0) * 1e3 / 2
+    extra["cfg2_host_io"] = {"workload": "cfg 2 f32 via ku_eval_many (host feeds in, host tensors out)",
+                             "ms_per_step": host_ms, "gbs": head["algo_bytes"] / (host_ms * 1e-3) / 1e9}
     if "2" in cfgs:
         b16 = bench_cfg2(hip, args.steps, args.warmup, "bf16")
         b16.pop("_graph")
