@@ -334,7 +334,4 @@ void launch_gemm_mfma(const GemmArgs& a, hipStream_t s) {
   }
 }
 
-bool attention_mfma_ok(const AttnArgs&) { return false; }
-void launch_attention_mfma(const AttnArgs&, hipStream_t) {}
-
 }  // namespace ku::hipbk

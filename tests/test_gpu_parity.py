@@ -160,21 +160,73 @@ def test_cfg3_batched_gemm_matches_oracle(hip):
 
 # ---------------- config 4: causal attention ----------------
 
+def f16_tensor(x: np.ndarray) -> Tensor:
+    return Tensor(DType.F16, x.shape, x.astype(np.float16).tobytes())
+
+
+def attention_graph(shape, dt, causal, fused):
+    g = Graph()
+    q, k, v = (g.input(list(shape), dt) for _ in range(3))
+    o = g.sdpa_fused(q, k, v, causal) if fused else g.sdpa_decomposed(q, k, v, causal)
+    return g, q, k, v, o
+
+
 @pytest.mark.parametrize("fused", [True, False])
-@pytest.mark.parametrize("b,h,s,d", [(1, 2, 128, 128), (2, 2, 80, 64)])
+@pytest.mark.parametrize("b,h,s,d", [(1, 2, 128, 128), (2, 2, 80, 64), (1, 3, 300, 128), (2, 4, 512, 64),
+                                     (1, 1, 64, 32)])
 def test_cfg4_attention_matches_oracle(hip, fused, b, h, s, d):
     print(f"cfg4 fused={fused} {b},{h},{s},{d}", flush=True)
-    g = Graph()
-    q = g.input([b, h, s, d], DType.BF16)
-    k = g.input([b, h, s, d], DType.BF16)
-    v = g.input([b, h, s, d], DType.BF16)
-    o = g.sdpa_fused(q, k, v, True) if fused else g.sdpa_decomposed(q, k, v, True)
+    g, q, k, v, o = attention_graph([b, h, s, d], DType.BF16, True, fused)
     feeds = {q: bf16_tensor(randn([b, h, s, d], 41)), k: bf16_tensor(randn([b, h, s, d], 42)),
              v: bf16_tensor(randn([b, h, s, d], 43))}
     got = to_f32(hip.eval_with(g, o, feeds))
     want = to_f32(interpret(g, [o], feeds)[0])
     assert rel_err(got, want) <= 1e-2
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="attention")
+
+
+@pytest.mark.parametrize("dt,causal,s", [(DType.F16, True, 256), (DType.BF16, False, 200), (DType.F16, False, 64)])
+def test_attention_dtypes_and_non_causal_match_oracle(hip, dt, causal, s):
+    print(f"attention dt={dt} causal={causal} s={s}", flush=True)
+    shape = [1, 2, s, 128]
+    g, q, k, v, o = attention_graph(shape, dt, causal, True)
+    mk = f16_tensor if dt == DType.F16 else bf16_tensor
+    feeds = {q: mk(randn(shape, 51)), k: mk(randn(shape, 52)), v: mk(randn(shape, 53))}
+    got = to_f32(hip.eval_with(g, o, feeds))
+    want = to_f32(interpret(g, [o], feeds)[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="attention")
+
+
+def test_attention_full_size_mfma_agrees_with_rowwise_kernel(hip, monkeypatch):
+    # cfg 4 at its real shape: the MFMA flash kernel against the independent one-query-per-thread
+    # kernel (f32 dot products, no MFMA), which the small-shape tests pin to the oracle
+    print("cfg4 full size mfma vs rowwise", flush=True)
+    shape = [4, 32, 2048, 128]
+    g, q, k, v, o = attention_graph(shape, DType.BF16, True, True)
+    rng = np.random.default_rng(7)
+    feeds = {n: bf16_tensor(rng.standard_normal(shape, dtype=np.float32)) for n in (q, k, v)}
+    assert "attn_mfma" in hip.plan(g, [o], feeds).steps()[0]
+    fast = to_f32(hip.eval_with(g, o, feeds))
+    monkeypatch.setenv("KURUMI_HIP_NO_MFMA", "1")
+    g2, q2, k2, v2, o2 = attention_graph(shape, DType.BF16, True, True)
+    slow = to_f32(hip.eval_with(g2, o2, {q2: feeds[q], k2: feeds[k], v2: feeds[v]}))
+    assert np.isfinite(fast).all()
+    assert_close(fast, slow, rtol=1e-2, atol=1e-2 * np.abs(slow).max(), what="attention mfma vs rowwise")
+
+
+def test_attention_causal_prefix_invariance(hip):
+    # causality: changing keys/values after position p leaves outputs of queries <= p bit-identical
+    shape, p = [1, 4, 1024, 128], 700
+    g, q, k, v, o = attention_graph(shape, DType.BF16, True, True)
+    rng = np.random.default_rng(8)
+    qv, kv, vv = (rng.standard_normal(shape, dtype=np.float32) for _ in range(3))
+    a = to_f32(hip.eval_with(g, o, {q: bf16_tensor(qv), k: bf16_tensor(kv), v: bf16_tensor(vv)}))
+    kv2, vv2 = kv.copy(), vv.copy()
+    kv2[:, :, p + 1:] = rng.standard_normal(kv2[:, :, p + 1:].shape, dtype=np.float32) * 3
+    vv2[:, :, p + 1:] = -vv2[:, :, p + 1:]
+    b = to_f32(hip.eval_with(g, o, {q: bf16_tensor(qv), k: bf16_tensor(kv2), v: bf16_tensor(vv2)}))
+    np.testing.assert_array_equal(a[:, :, :p + 1], b[:, :, :p + 1])
+    assert not np.array_equal(a[:, :, p + 1:], b[:, :, p + 1:])
 
 
 def test_attention_first_query_sees_first_key(hip):
