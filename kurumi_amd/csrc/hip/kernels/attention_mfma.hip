@@ -16,8 +16,8 @@
 // holds key 8*(i/4) + 4*h + i%4, i.e. key k sits at slot swap(bit2, bit3)(k). V^T is written to
 // LDS in that slot order, so both operands read 16 contiguous bytes per lane.
 //
-// Work-group: NW waves, 32*NW queries, blocks of BK = 64 keys staged global -> registers -> LDS
-// (K row-major, V transposed), double-buffered with one barrier per block. Causal q-tiles are
+// Work-group: NW waves of 32*QT queries each, blocks of BK = 64 keys staged global -> registers
+// -> LDS (K row-major, V transposed), double-buffered with one barrier per block. Causal q-tiles are
 // issued heaviest first, and every head's tiles land on one XCD so its K/V stay in that L2.
 #include <hip/hip_runtime.h>
 
@@ -37,6 +37,9 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int BK = 64;  // keys per block
 constexpr float LOG2E = 1.4426950408889634f;
@@ -51,24 +54,58 @@ __device__ __forceinline__ f32x16 mfma(const u32x4& a, const u32x4& b, const f32
                                                   0, 0);
 }
 
-// two f32 -> one dword of two 16-bit values (round to nearest even)
+// two f32 -> one dword of two 16-bit values, rounded to nearest even by v_cvt_pk_bf16_f32 /
+// v_cvt_f16_f32 (the probabilities and outputs here are never NaN unless an input is)
 template <int DT>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  if constexpr (DT == GT_BF16) return (uint32_t)d_bf16_st(lo) | ((uint32_t)d_bf16_st(hi) << 16);
-  else return (uint32_t)d_f16_st(lo) | ((uint32_t)d_f16_st(hi) << 16);
+  const f32x2 v = {lo, hi};
+  if constexpr (DT == GT_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
 
+// c + lo + hi of a packed pair of 16-bit floats (v_dot2c_f32_{bf16,f16} against 1.0 pairs)
 template <int DT>
-__device__ __forceinline__ uint16_t st16(float v) {
-  if constexpr (DT == GT_BF16) return d_bf16_st(v);
-  else return d_f16_st(v);
+__device__ __forceinline__ float sum2(uint32_t pair, float c) {
+  if constexpr (DT == GT_BF16) {
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, c, false);
+  } else {
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), one, c, false);
+  }
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p, uint32_t bytes) {
+  // dword3 0x00020000: 32-bit data format, the raw-buffer setting for gfx9 parts
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
 __device__ __forceinline__ int key_slot(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
-template <int D, int DT, int NW>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2))) attn_mfma_k(AttnArgs a) {
-  constexpr int NT = NW * 64, BQ = 32 * NW;
+// Lazy rescaling: the running max m (kept pre-multiplied by scale*log2 e) only moves when a
+// block's max exceeds it by more than RESCALE (log2 units), so most blocks skip the O rescale.
+// Probabilities then reach at most 2^RESCALE before normalisation, far inside f32 and bf16 range;
+// the result is the same softmax (numerator and denominator share the stale max).
+constexpr float RESCALE = 8.f;
+
+// Scheduling hints (llvm.amdgcn.sched.group.barrier masks): interleave the MFMAs of one product
+// with the VALU work of the softmax, so the matrix core and the vector ALU run side by side.
+constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_DSR = 0x100, SG_DSW = 0x200;
+
+// QT 32-query tiles per wave: QT = 2 halves the LDS bytes per MFMA (every K / V fragment feeds
+// two MFMAs) at the price of one wave per SIMD.
+//
+// Software pipeline per block kb (one barrier each): the S^T MFMAs of block kb+1 are issued
+// between the softmax instructions of block kb; then the P.V MFMAs of block kb run while the
+// staged K of block kb+2 and V of block kb+1 are written to LDS. K and V have separate
+// double buffers, K one block ahead of V.
+template <int D, int DT, int NW, int QT>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 2 : 1, QT == 1 ? 2 : 1)))
+attn_mfma_k(AttnArgs a) {
+  constexpr int NT = NW * 64, QW = 32 * QT, BQ = QW * NW;
   constexpr int KROW = D * 2 + 16;   // LDS bytes per K row (padded)
   constexpr int VROW = BK * 2 + 16;  // LDS bytes per V^T row (padded)
   constexpr int KBYTES = BK * KROW, VBYTES = D * VROW;
@@ -78,7 +115,11 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   constexpr int DTL = D / 32;          // 32-row tiles of O^T
   static_assert(KC >= 1 && KC * NT * 8 == BK * D, "K staging");
   static_assert(R >= 1 && R <= 4 && (R & (R - 1)) == 0 && R * NT * 8 == BK * D, "V staging");
-  __shared__ __attribute__((aligned(16))) unsigned char lds[2][KBYTES + VBYTES];
+  // every block a wave needs starts at or before the wave's first query, so a lane is never
+  // fully masked in a block it needs
+  static_assert(BK % 32 == 0 && (QW % BK == 0 || BK % QW == 0), "block / wave alignment");
+  __shared__ __attribute__((aligned(16))) unsigned char ldsk[2][KBYTES];
+  __shared__ __attribute__((aligned(16))) unsigned char ldsv[2][VBYTES];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, qc = lane & 31;
   const int64_t S = a.s;
@@ -88,168 +129,240 @@ __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2,
   const int head = id % (int)a.bh;
   const int qt = a.causal ? nqt - 1 - id / (int)a.bh : id / (int)a.bh;
   const int64_t q0 = (int64_t)qt * BQ;
-  const int64_t qw = q0 + wave * 32;  // first query of this wave
-  const int64_t qi = qw + qc;         // this lane's query
+  const int64_t qw = q0 + wave * QW;  // first query of this wave
   const int64_t base = (int64_t)head * S * D;
-  const uint16_t* Q = static_cast<const uint16_t*>(a.q) + base;
-  const uint16_t* K = static_cast<const uint16_t*>(a.k) + base;
-  const uint16_t* V = static_cast<const uint16_t*>(a.v) + base;
+  // raw buffer loads: rows past the sequence read as zero, no branches
+  const uint32_t hb = (uint32_t)(S * D * 2);  // bytes per head
+  const auto Q = rsrc(static_cast<const uint16_t*>(a.q) + base, hb);
+  const auto K = rsrc(static_cast<const uint16_t*>(a.k) + base, hb);
+  const auto V = rsrc(static_cast<const uint16_t*>(a.v) + base, hb);
 
-  // Q fragments (B operand of S^T): lane holds q = qi, dims 16*s + 8*h .. +7
-  u32x4 qf[DS];
+  // Q fragments (B operand of S^T): lane holds query qw + 32u + qc, dims 16*s + 8*h .. +7
+  u32x4 qf[QT][DS];
 #pragma unroll
-  for (int s = 0; s < DS; ++s)
-    qf[s] = qi < S ? *reinterpret_cast<const u32x4*>(Q + qi * D + s * 16 + h * 8) : u32x4{0, 0, 0, 0};
+  for (int u = 0; u < QT; ++u) {
+    const int64_t qi = qw + 32 * u + qc;
+    const uint32_t off = qi < S ? (uint32_t)(qi * D * 2) + h * 16 : hb;
+#pragma unroll
+    for (int s = 0; s < DS; ++s) qf[u][s] = bload(Q, off + s * 32);
+  }
 
   const int64_t kend = a.causal ? (q0 + BQ < S ? q0 + BQ : S) : S;  // keys this tile needs
   const int nkb = (int)((kend + BK - 1) / BK);
 
   u32x4 rk[KC], rv[R];
-  auto load = [&](int kb) {
-    const int64_t k0 = (int64_t)kb * BK;
+  // V staging: lanes with consecutive ids take consecutive key groups of one 8-dim chunk, so the
+  // transposed LDS writes of a 16-lane group fill one V^T row without bank conflicts
+  const int dc = tid / (BK / R), kq = tid % (BK / R);
+  // a block past nkb loads from offset hb (zeros) instead of branching
+  auto loadK = [&](int kb) {
+    const uint32_t k0b = kb < nkb ? (uint32_t)kb * BK * D * 2 : hb;
 #pragma unroll
     for (int i = 0; i < KC; ++i) {
       const int c = tid + i * NT, row = c / (D / 8), col = c % (D / 8);
-      rk[i] = (k0 + row < S) ? *reinterpret_cast<const u32x4*>(K + (k0 + row) * D + col * 8) : u32x4{0, 0, 0, 0};
-    }
-    const int dc = tid % (D / 8), kq = tid / (D / 8);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t kk = k0 + kq * R + r;
-      rv[r] = kk < S ? *reinterpret_cast<const u32x4*>(V + kk * D + dc * 8) : u32x4{0, 0, 0, 0};
+      rk[i] = bload(K, k0b + row * D * 2 + col * 16);
     }
   };
-  auto store = [&](int buf) {
-    unsigned char* L = lds[buf];
+  auto loadV = [&](int kb) {
+    const uint32_t k0b = kb < nkb ? (uint32_t)kb * BK * D * 2 : hb;
+#pragma unroll
+    for (int r = 0; r < R; ++r) rv[r] = bload(V, k0b + (kq * R + r) * D * 2 + dc * 16);
+  };
+  auto storeK = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < KC; ++i) {
       const int c = tid + i * NT, row = c / (D / 8), col = c % (D / 8);
-      *reinterpret_cast<u32x4*>(L + row * KROW + col * 16) = rk[i];
+      *reinterpret_cast<u32x4*>(ldsk[buf] + row * KROW + col * 16) = rk[i];
     }
-    // R keys x 8 dims -> 8 V^T rows x R key slots (R keys starting at a multiple of R stay
-    // contiguous under the slot permutation because R <= 4)
-    unsigned char* LV = L + KBYTES;
-    const int dc = tid % (D / 8), kq = tid / (D / 8);
+  };
+  // R keys x 8 dims -> 8 V^T rows x R key slots (R keys starting at a multiple of R stay
+  // contiguous under the slot permutation because R <= 4)
+  auto storeV = [&](int buf) {
     const int slot = (kq * R & ~15) | key_slot((kq * R) & 15);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int w = j >> 1, sh = (j & 1) * 16;
-      unsigned char* dst = LV + (dc * 8 + j) * VROW + slot * 2;
+      // dims 2w (low halves) or 2w+1 (high halves) of R consecutive keys, paired by v_perm_b32
+      const int w = j >> 1;
+      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+      unsigned char* dst = ldsv[buf] + (dc * 8 + j) * VROW + slot * 2;
       if constexpr (R == 4) {
-        uint32_t o0 = ((rv[0][w] >> sh) & 0xffffu) | (((rv[1][w] >> sh) & 0xffffu) << 16);
-        uint32_t o1 = ((rv[2][w] >> sh) & 0xffffu) | (((rv[3][w] >> sh) & 0xffffu) << 16);
-        *reinterpret_cast<u32x2*>(dst) = u32x2{o0, o1};
+        *reinterpret_cast<u32x2*>(dst) =
+            u32x2{__builtin_amdgcn_perm(rv[1][w], rv[0][w], sel), __builtin_amdgcn_perm(rv[3][w], rv[2][w], sel)};
       } else if constexpr (R == 2) {
-        *reinterpret_cast<uint32_t*>(dst) = ((rv[0][w] >> sh) & 0xffffu) | (((rv[1][w] >> sh) & 0xffffu) << 16);
+        *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(rv[1][w], rv[0][w], sel);
       } else {
-        *reinterpret_cast<uint16_t*>(dst) = (uint16_t)((rv[0][w] >> sh) & 0xffffu);
+        *reinterpret_cast<uint16_t*>(dst) = (uint16_t)((rv[0][w] >> ((j & 1) * 16)) & 0xffffu);
       }
     }
   };
-
-  f32x16 o[DTL];
+  // S^T of one block from a K buffer: 2 key tiles x QT query tiles, DS k-steps
+  auto s_mfma = [&](const unsigned char* L, f32x16 (&sc)[QT][2]) {
 #pragma unroll
-  for (int t = 0; t < DTL; ++t)
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int v = 0; v < 16; ++v) o[t][v] = 0.f;
-  float m = -INFINITY, l = 0.f;
-  const float c = a.scale * LOG2E;
-
-  load(0);
-  store(0);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int cur = kb & 1;
-    if (kb + 1 < nkb) load(kb + 1);
-    const int64_t k0 = (int64_t)kb * BK;
-    // wave-uniform: skip blocks entirely above this wave's diagonal
-    const bool active = !a.causal || k0 <= qw + 31;
-    if (active && qw < S) {
-      const unsigned char* L = lds[cur];
-      f32x16 sc[2];
+      for (int u = 0; u < QT; ++u)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) sc[u][t][v] = 0.f;
+#pragma unroll
+    for (int s = 0; s < DS; ++s)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(L + (t * 32 + qc) * KROW + s * 32 + h * 16);
 #pragma unroll
-        for (int v = 0; v < 16; ++v) sc[t][v] = 0.f;
-#pragma unroll
-        for (int s = 0; s < DS; ++s) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(L + (t * 32 + qc) * KROW + s * 32 + h * 16);
-          sc[t] = mfma<DT>(kf, qf[s], sc[t]);
-        }
+        for (int u = 0; u < QT; ++u) sc[u][t] = mfma<DT>(kf, qf[u][s], sc[u][t]);
       }
-      // mask: keys past the sequence, and (causal) keys after the query
-      const bool need_mask = (k0 + BK > S) || (a.causal && k0 + BK - 1 > qw);
-      if (need_mask) {
+  };
+
+  f32x16 o[QT][DTL];
+  float mc[QT], l[QT];
+#pragma unroll
+  for (int u = 0; u < QT; ++u) {
+    mc[u] = -INFINITY;
+    l[u] = 0.f;
+#pragma unroll
+    for (int t = 0; t < DTL; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[u][t][v] = 0.f;
+  }
+  const float c = a.scale * LOG2E;
+  const bool live = qw < S;  // wave-uniform: waves past the sequence only help staging
+
+  loadK(0);
+  loadV(0);
+  storeK(0);
+  storeV(0);
+  loadK(1);
+  storeK(1);
+  __syncthreads();
+  f32x16 sc[QT][2];
+  s_mfma(ldsk[0], sc);
+
+  for (int kb = 0; kb < nkb; ++kb) {
+    loadK(kb + 2);
+    loadV(kb + 1);
+    const int64_t k0 = (int64_t)kb * BK;
+    f32x16 sn[QT][2];
+    u32x4 pf[QT][4];
+    if (live) {
+#pragma unroll
+      for (int u = 0; u < QT; ++u) {
+        // mask keys past the sequence and (causal) keys after the query: key k0 + off(t, v) + 4h
+        // is dropped when off(t, v) > lim, off(t, v) = 32t + 8(v/4) + v%4 a constant per register
+        if ((k0 + BK > S) || (a.causal && k0 + BK - 1 > qw + 32 * u)) {
+          const int64_t qi = qw + 32 * u + qc;
+          const int64_t last = a.causal && qi < S - 1 ? qi : S - 1;  // last visible key
+          const int lim = (int)(last - k0) - 4 * h;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int v = 0; v < 16; ++v)
+              if (t * 32 + (v >> 2) * 8 + (v & 3) > lim) sc[u][t][v] = -INFINITY;
+        }
+        float bm = sc[u][0][0];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) {
-            const int64_t kk = k0 + t * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-            if (kk >= S || (a.causal && kk > qi)) sc[t][v] = -INFINITY;
-          }
-      }
-      float bm = sc[0][0];
+          for (int v = 0; v < 16; ++v) bm = fmaxf(bm, sc[u][t][v]);
+        // the two halves of the wave hold the same queries: exchange without LDS
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), false, false);
+        bm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+        // both halves see the same bm and mc, so they take the same decision
+        if (__builtin_amdgcn_ballot_w64(bm > mc[u] + RESCALE) != 0) {
+          const float mn = fmaxf(mc[u], bm);
+          const float corr = __builtin_amdgcn_exp2f(mc[u] - mn);
+          mc[u] = mn;
+          l[u] *= corr;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+          for (int t = 0; t < DTL; ++t)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) bm = fmaxf(bm, sc[t][v]);
-      bm = fmaxf(bm, __shfl_xor(bm, 32));
-      const float mn = fmaxf(m, bm);
-      const float mb = mn == -INFINITY ? 0.f : mn * c;
-      const float corr = __builtin_amdgcn_exp2f(m * c - mb);
-      m = mn;
-      float rs = 0.f;
-      u32x4 pf[4];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int v2 = 0; v2 < 8; ++v2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[t][2 * v2], c, -mb));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[t][2 * v2 + 1], c, -mb));
-          rs += p0 + p1;
-          // step s = 2t + v2/4 takes v = 8*(s%2) .. +7 of tile t
-          pf[2 * t + (v2 >> 2)][v2 & 3] = pack2<DT>(p0, p1);
+            for (int v = 0; v < 16; ++v) o[u][t][v] *= corr;
         }
-      l = l * corr + rs;
+      }
+      // S^T of block kb+1 (its K is already in LDS) interleaved with the exponentials of block kb
+      s_mfma(ldsk[(kb + 1) & 1], sn);
 #pragma unroll
-      for (int t = 0; t < DTL; ++t)
+      for (int u = 0; u < QT; ++u) {
+        // the row sum adds the rounded probabilities (the ones the P.V product uses), two at a
+        // time with v_dot2 against (1, 1), in two chains
+        float rs[2] = {0.f, 0.f};
 #pragma unroll
-        for (int v = 0; v < 16; ++v) o[t][v] *= corr;
-      const unsigned char* LV = L + KBYTES;
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int v2 = 0; v2 < 8; ++v2) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[u][t][2 * v2], c, -mc[u]));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[u][t][2 * v2 + 1], c, -mc[u]));
+            const uint32_t pp = pack2<DT>(p0, p1);
+            rs[v2 & 1] = sum2<DT>(pp, rs[v2 & 1]);
+            // step s = 2t + v2/4 takes v = 8*(s%2) .. +7 of tile t
+            pf[u][2 * t + (v2 >> 2)][v2 & 3] = pp;
+          }
+        l[u] += rs[0] + rs[1];
+      }
+#pragma unroll
+      for (int i = 0; i < DS * 2; ++i) {
+        __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_MFMA, QT, 0);
+        __builtin_amdgcn_sched_group_barrier(SG_VALU, 96 * QT / (DS * 2), 0);
+      }
+      // O^T += V^T . P^T for block kb
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int t = 0; t < DTL; ++t) {
-          const u32x4 vf = *reinterpret_cast<const u32x4*>(LV + (t * 32 + qc) * VROW + s * 32 + h * 16);
-          o[t] = mfma<DT>(vf, pf[s], o[t]);
+          const u32x4 vf = *reinterpret_cast<const u32x4*>(ldsv[kb & 1] + (t * 32 + qc) * VROW + s * 32 + h * 16);
+#pragma unroll
+          for (int u = 0; u < QT; ++u) o[u][t] = mfma<DT>(vf, pf[u][s], o[u][t]);
         }
     }
-    if (kb + 1 < nkb) store(cur ^ 1);
+    // stage K of block kb+2 and V of block kb+1 into the buffers freed by the previous block
+    storeK(kb & 1);
+    storeV((kb + 1) & 1);
     __syncthreads();
+#pragma unroll
+    for (int u = 0; u < QT; ++u)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) sc[u][t] = sn[u][t];
   }
 
-  if (qi >= S) return;
-  l += __shfl_xor(l, 32);
-  const float inv = 1.f / l;
-  uint16_t* O = static_cast<uint16_t*>(a.o) + base + qi * D;
 #pragma unroll
-  for (int t = 0; t < DTL; ++t)
+  for (int u = 0; u < QT; ++u) {
+    const int64_t qi = qw + 32 * u + qc;
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l[u]), __float_as_uint(l[u]), false, false);
+    const float lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    if (qi >= S) continue;
+    const float inv = 1.f / lt;
+    uint16_t* O = static_cast<uint16_t*>(a.o) + base + qi * D;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = t * 32 + g * 8 + h * 4;
-      u32x2 w;
-      w[0] = pack2<DT>(o[t][4 * g] * inv, o[t][4 * g + 1] * inv);
-      w[1] = pack2<DT>(o[t][4 * g + 2] * inv, o[t][4 * g + 3] * inv);
-      *reinterpret_cast<u32x2*>(O + d0) = w;
-    }
+    for (int t = 0; t < DTL; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = t * 32 + g * 8 + h * 4;
+        u32x2 w;
+        w[0] = pack2<DT>(o[u][t][4 * g] * inv, o[u][t][4 * g + 1] * inv);
+        w[1] = pack2<DT>(o[u][t][4 * g + 2] * inv, o[u][t][4 * g + 3] * inv);
+        *reinterpret_cast<u32x2*>(O + d0) = w;
+      }
+  }
+}
+
+int attn_qt() {
+  static const int q = [] {
+    const char* e = std::getenv("KURUMI_HIP_ATTN_QT");
+    return (e && e[0] == '2') ? 2 : 1;
+  }();
+  return q;
 }
 
 template <int D, int DT>
 void launch_d(const AttnArgs& a, hipStream_t s) {
   constexpr int NW = 4;
-  const int64_t nqt = (a.s + 32 * NW - 1) / (32 * NW);
-  dim3 grid((unsigned)(nqt * a.bh));
-  hipLaunchKernelGGL((attn_mfma_k<D, DT, NW>), grid, dim3(NW * 64), 0, s, a);
+  if (attn_qt() == 2) {
+    const int64_t nqt = (a.s + 64 * NW - 1) / (64 * NW);
+    hipLaunchKernelGGL((attn_mfma_k<D, DT, NW, 2>), dim3((unsigned)(nqt * a.bh)), dim3(NW * 64), 0, s, a);
+  } else {
+    const int64_t nqt = (a.s + 32 * NW - 1) / (32 * NW);
+    hipLaunchKernelGGL((attn_mfma_k<D, DT, NW, 1>), dim3((unsigned)(nqt * a.bh)), dim3(NW * 64), 0, s, a);
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -261,6 +374,7 @@ bool attention_mfma_ok(const AttnArgs& a) {
   if (!(a.dtype == GT_BF16 || a.dtype == GT_F16)) return false;
   if (!(a.d == 64 || a.d == 128)) return false;
   if (a.s <= 0 || a.bh <= 0 || a.bh * ((a.s + 127) / 128) > 0x7fffffff) return false;
+  if (a.s * a.d * 2 >= (int64_t(1) << 31)) return false;  // per-head buffer offsets are 32-bit
   if (a.q && (!aligned16(a.q) || !aligned16(a.k) || !aligned16(a.v) || !aligned16(a.o))) return false;
   return true;
 }
