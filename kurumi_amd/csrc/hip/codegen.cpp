@@ -14,6 +14,7 @@
 // kurumi_metal/src/backend/fuse/emit.rs:80-142.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstdio>
 #include <functional>
 #include <map>
@@ -99,7 +100,8 @@ std::string cast_expr(DType from, DType to, const std::string& x) {
   std::string dx = "((double)(" + x + "))";
   switch (to) {
     case DType::F32:
-      if (ffrom) return x;
+      // the reference widens through f64, which quiets a signalling NaN
+      if (ffrom) return "quiet_nan(" + x + ")";
       return "((float)" + dx + ")";
     case DType::F64: return dx;
     case DType::BF16: return ffrom ? "rbf16(" + x + ")" : "rbf16_d(" + dx + ")";
@@ -169,6 +171,7 @@ struct Gen {
   std::vector<int> first_phase;    // per node: first phase computing it
   bool has_final = false;
   bool unroll = false;
+  int min_waves = 1;  // amdgpu_waves_per_eu lower bound of a line kernel
 
   Gen(const Region& r, const std::vector<Slot>& s, int i) : R(r), slots(s), index(i) {}
 
@@ -193,6 +196,15 @@ struct Gen {
   void plan_layout();
   void schedule();
   void emit_leaf_load(int ni, const std::string& c_expr);
+  void emit_leaf_convert(int ni);
+  // argmax/argmin index type along the line (32-bit unless the line is that long)
+  // 16-bit leaves are cached two to a 32-bit register
+  bool packed_cache(int c) const {
+    const RNode& cn = node(c);
+    return cn.kind == RK_LEAF && dt_width(R.leaves[cn.leaf].dtype) == 2 && V % 2 == 0;
+  }
+  std::string aix() const { return L >= ((uint64_t)1 << 31) ? "i64" : "i32"; }
+  std::string aix_none() const { return L >= ((uint64_t)1 << 31) ? "(i64)9223372036854775807ll" : "(i32)2147483647"; }
   void emit_full_node(int ni, int phase, const std::string& c_expr);
   void emit_line_node(int ni);
   void emit_red_init(int ni);
@@ -378,42 +390,41 @@ void Gen::schedule() {
     if (is_red(n.kind)) red_inputs.insert(n.in[0]);
   unroll = !flat && NC <= 16;
   if (!flat && NC <= 16) {
-    // Greedy register budget: values feeding later reductions first (latest level first),
-    // then leaves; a candidate only counts while some later phase still has to recompute it.
-    std::vector<int> cand;
-    for (auto& kv : uses)
-      if (kv.second >= 2 && (node(kv.first).kind == RK_LEAF || red_inputs.count(kv.first))) cand.push_back(kv.first);
-    std::sort(cand.begin(), cand.end(), [&](int x, int y) {
-      bool rx = red_inputs.count(x), ry = red_inputs.count(y);
-      if (rx != ry) return rx;
-      return node(x).level > node(y).level;
-    });
-    int regs = 0;
-    for (int c : cand) {
-      int cost = NC * V * (node(c).dtype == DType::F64 || dt_width(node(c).dtype) == 8 ? 2 : 1);
-      // skip a leaf whose every later use already reads a cached descendant
-      bool still_needed = true;
-      if (node(c).kind == RK_LEAF) {
-        std::vector<std::set<int>> trial(nph + 2);
-        std::function<void(int, int)> walk = [&](int p, int n) {
-          if (!full(n) || trial[p].count(n)) return;
-          trial[p].insert(n);
-          if (cached.count(n) && first_phase[n] < p) return;
-          for (int i : node(n).in) walk(p, i);
-        };
-        for (size_t i = 0; i < R.nodes.size(); ++i) {
-          if (is_red(R.nodes[i].kind)) walk(R.nodes[i].level, R.nodes[i].in[0]);
-          if (store_phase[i]) walk(store_phase[i], (int)i);
-        }
-        int phases = 0;
-        for (int p = 1; p <= nph; ++p) phases += trial[p].count(c) ? 1 : 0;
-        still_needed = phases >= 2;
-      }
-      if (still_needed && regs + cost <= 160) {
-        cached.insert(c);
-        regs += cost;
-      }
+    // Register budget: keep at least two work-groups resident per CU (a line kernel's phases
+    // are load-bound then ALU/store-bound, so a second line in flight overlaps them). With
+    // W waves per group that is W/2 waves per SIMD out of 512 VGPRs, minus ~28 for the rest.
+    int waves_per_simd = std::max(1, WG / 128);
+    int limit = std::min(256, (512 / waves_per_simd) / 8 * 8);
+    min_waves = waves_per_simd;
+    if (const char* e = std::getenv("KURUMI_HIP_LINE_WAVES")) min_waves = std::atoi(e);
+    int budget = limit - 28;
+    if (const char* e = std::getenv("KURUMI_HIP_CACHE_BUDGET")) budget = std::atoi(e);
+    auto cost_of = [&](int c) {
+      // half-registers per value: 16-bit leaves are cached two to a register
+      int per = packed_cache(c) ? 1 : (dt_width(node(c).dtype) == 8 ? 4 : 2);
+      return (NC * V * per + 1) / 2;
+    };
+    // Leaves first: a leaf needed by two phases and not cached is read from HBM twice, while an
+    // uncached intermediate only costs ALU to recompute from cached leaves. Then values feeding
+    // later reductions (latest level first).
+    std::vector<int> leaves_c, inter_c;
+    for (auto& kv : uses) {
+      if (kv.second < 2) continue;
+      if (node(kv.first).kind == RK_LEAF) leaves_c.push_back(kv.first);
+      else if (red_inputs.count(kv.first)) inter_c.push_back(kv.first);
     }
+    std::sort(inter_c.begin(), inter_c.end(), [&](int x, int y) { return node(x).level > node(y).level; });
+    int regs = 0;
+    for (int c : leaves_c)
+      if (regs + cost_of(c) <= budget) {
+        cached.insert(c);
+        regs += cost_of(c);
+      }
+    for (int c : inter_c)
+      if (regs + cost_of(c) <= budget) {
+        cached.insert(c);
+        regs += cost_of(c);
+      }
   }
   // with caches, later phases need fewer recomputations: rebuild need sets
   if (!cached.empty()) {
@@ -457,37 +468,55 @@ void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
   std::string T = stype(l.dtype), C = ctype(l.dtype);
   std::string P = "p" + std::to_string(slot_param.at(l.slot));
   std::string base = "b" + std::to_string(n.leaf);
-  o << "      " << C << " f" << ni << "[" << V << "];\n";
+  // r<ni>: the stored bits (what a leaf cache keeps), f<ni>: the compute values
+  o << "      " << T << " r" << ni << "[" << V << "];\n";
   if (leaf_vec[n.leaf]) {
     o << "      { VecT<" << T << ", " << V << "> raw = *(const VecT<" << T << ", " << V << ">*)((const " << T << "*)" << P
       << " + " << base << " + (" << ix() << ")(" << c_expr << "));\n";
-    o << "        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) f" << ni << "[j] = " << ld(l.dtype, "raw.v[j]")
-      << "; }\n";
-    return;
-  }
-  int64_t sa = v.strides[vecaxis];
-  o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) {\n";
-  std::string coord = "((i64)(" + c_expr + ") + j)";
-  std::string off = base + " + (" + ix() + ")(";
-  if (v.padded()) off += "(" + coord + " - " + std::to_string(v.plo[vecaxis]) + ")";
-  else off += coord;
-  off += " * " + std::to_string(sa) + "ll)";
-  std::string load = ld(l.dtype, "((const " + T + "*)" + P + ")[" + off + "]");
-  if (v.padded()) {
-    std::string inr = "(vb" + std::to_string(n.leaf) + " && " + coord + " >= " + std::to_string(v.plo[vecaxis]) +
-                      " && " + coord + " < " + std::to_string(v.plo[vecaxis] + (int64_t)v.src_shape[vecaxis]) + ")";
-    o << "        f" << ni << "[j] = " << inr << " ? " << load << " : (" << C << ")0;\n";
+    o << "        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = raw.v[j]; }\n";
   } else {
-    o << "        f" << ni << "[j] = " << load << ";\n";
+    int64_t sa = v.strides[vecaxis];
+    o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) {\n";
+    std::string coord = "((i64)(" + c_expr + ") + j)";
+    std::string off = base + " + (" + ix() + ")(";
+    if (v.padded()) off += "(" + coord + " - " + std::to_string(v.plo[vecaxis]) + ")";
+    else off += coord;
+    off += " * " + std::to_string(sa) + "ll)";
+    std::string load = "((const " + T + "*)" + P + ")[" + off + "]";
+    if (v.padded()) {
+      std::string inr = "(vb" + std::to_string(n.leaf) + " && " + coord + " >= " + std::to_string(v.plo[vecaxis]) +
+                        " && " + coord + " < " + std::to_string(v.plo[vecaxis] + (int64_t)v.src_shape[vecaxis]) + ")";
+      o << "        r" << ni << "[j] = " << inr << " ? " << load << " : (" << T << ")0;\n";
+    } else {
+      o << "        r" << ni << "[j] = " << load << ";\n";
+    }
+    o << "      }\n";
   }
-  o << "      }\n";
+  emit_leaf_convert(ni);
+}
+
+void Gen::emit_leaf_convert(int ni) {
+  const Leaf& l = R.leaves[node(ni).leaf];
+  o << "      " << ctype(l.dtype) << " f" << ni << "[" << V << "];\n";
+  o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) f" << ni << "[j] = "
+    << ld(l.dtype, "r" + std::to_string(ni) + "[j]") << ";\n";
 }
 
 void Gen::emit_full_node(int ni, int phase, const std::string& c_expr) {
   const RNode& n = node(ni);
   bool from_cache = cached.count(ni) && first_phase[ni] < phase;
   if (from_cache) {
-    o << "      " << ctype(n.dtype) << " (&f" << ni << ")[" << V << "] = cache" << ni << "[c];\n";
+    if (packed_cache(ni)) {
+      o << "      " << stype(R.leaves[n.leaf].dtype) << " r" << ni << "[" << V << "];\n";
+      o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = (u16)(cache" << ni
+        << "[c][j >> 1] >> ((j & 1) * 16));\n";
+      emit_leaf_convert(ni);
+    } else if (n.kind == RK_LEAF) {
+      o << "      " << stype(R.leaves[n.leaf].dtype) << " (&r" << ni << ")[" << V << "] = cache" << ni << "[c];\n";
+      emit_leaf_convert(ni);
+    } else {
+      o << "      " << ctype(n.dtype) << " (&f" << ni << ")[" << V << "] = cache" << ni << "[c];\n";
+    }
     return;
   }
   if (n.kind == RK_LEAF) {
@@ -518,8 +547,12 @@ void Gen::emit_full_node(int ni, int phase, const std::string& c_expr) {
       << ";\n";
   }
   if (cached.count(ni) && first_phase[ni] == phase) {
-    o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) cache" << ni << "[c][j] = f" << ni
-      << "[j];\n";
+    if (packed_cache(ni))
+      o << "      #pragma unroll\n      for (int j = 0; j < " << V / 2 << "; ++j) cache" << ni << "[c][j] = (u32)r" << ni
+        << "[2 * j] | ((u32)r" << ni << "[2 * j + 1] << 16);\n";
+    else
+      o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) cache" << ni << "[c][j] = "
+        << (n.kind == RK_LEAF ? "r" : "f") << ni << "[j];\n";
   }
 }
 
@@ -548,8 +581,8 @@ void Gen::emit_red_init(int ni) {
     std::string init;
     if (fvalued(in) || in == DType::F64) init = flt_lit(in == DType::F64 ? DType::F64 : DType::F32, mx ? -INFINITY : INFINITY);
     else init = mx ? int_min(in) : int_max(in);
-    o << "  " << ctype(in) << " bv" << r << " = " << init << "; i64 bi" << r << " = 9223372036854775807ll; bool bn" << r
-      << " = false;\n";
+    o << "  " << ctype(in) << " bv" << r << " = " << init << "; " << aix() << " bi" << r << " = " << aix_none()
+      << "; bool bn" << r << " = false;\n";
     return;
   }
   DType acc = n.dtype;
@@ -572,15 +605,14 @@ void Gen::emit_red_update(int ni, const std::string& k_expr, const std::string& 
   if (n.kind == (int)OpKind::ArgReduce) {
     bool mx = n.arg == ArgKind::Max;
     std::string cmp = mx ? ">" : "<";
-    std::string k = "((i64)(" + k_expr + "))";
-    if (fvalued(in) || in == DType::F64) {
-      o << "        { " << ctype(in) << " v_ = " << v << "; i64 k_ = " << k << "; if (k_ == 0 && v_ != v_) bn" << r
-        << " = true; if (v_ == v_ && (v_ " << cmp << " bv" << r << " || (v_ == bv" << r << " && k_ < bi" << r
-        << "))) { bv" << r << " = v_; bi" << r << " = k_; } }\n";
-    } else {
-      o << "        { " << ctype(in) << " v_ = " << v << "; i64 k_ = " << k << "; if (v_ " << cmp << " bv" << r
-        << " || (v_ == bv" << r << " && k_ < bi" << r << ")) { bv" << r << " = v_; bi" << r << " = k_; } }\n";
-    }
+    // A thread visits its elements in increasing k, so within the thread a strict comparison
+    // keeps the first index of equal values; NaN never compares true and is skipped. The
+    // reference's NaN-at-index-0 rule (the result is 0) is a flag set by the element k == 0.
+    std::string k = "((" + aix() + ")(" + k_expr + "))";
+    o << "        { " << ctype(in) << " v_ = " << v << "; if (v_ " << cmp << " bv" << r << ") { bv" << r
+      << " = v_; bi" << r << " = " << k << "; }";
+    if (fvalued(in) || in == DType::F64) o << " if (" << j << " == 0 && " << k << " == 0 && v_ != v_) bn" << r << " = true;";
+    o << " }\n";
     return;
   }
   bool fl = fvalued(n.dtype) || n.dtype == DType::F64 || in == DType::F32;
@@ -619,7 +651,7 @@ void Gen::emit_red_finish(int ni, int phase) {
   int wl = std::min(TPL, 64);
   for (int m = wl / 2; m >= 1; m /= 2) {
     if (arg)
-      o << "  { " << ctype(in) << " ov = shx(bv" << r << ", " << m << "); i64 oi = shx(bi" << r << ", " << m
+      o << "  { " << ctype(in) << " ov = shx(bv" << r << ", " << m << "); " << aix() << " oi = shx(bi" << r << ", " << m
         << "); bool on = shx(bn" << r << ", " << m << "); " << comb_arg("ov", "oi", "on") << " }\n";
     else
       o << "  { auto ov = shx(acc" << r << ", " << m << "); " << comb("ov") << " }\n";
@@ -628,13 +660,13 @@ void Gen::emit_red_finish(int ni, int phase) {
     int W = TPL / 64;
     std::string tag = std::to_string(phase) + "_" + r;
     if (arg) {
-      o << "  __shared__ " << ctype(in) << " lv" << tag << "[" << W << "]; __shared__ i64 li" << tag << "[" << W
+      o << "  __shared__ " << ctype(in) << " lv" << tag << "[" << W << "]; __shared__ " << aix() << " li" << tag << "[" << W
         << "]; __shared__ bool ln" << tag << "[" << W << "];\n";
       o << "  if ((threadIdx.x & 63) == 0) { lv" << tag << "[threadIdx.x >> 6] = bv" << r << "; li" << tag
         << "[threadIdx.x >> 6] = bi" << r << "; ln" << tag << "[threadIdx.x >> 6] = bn" << r << "; }\n";
       o << "  __syncthreads();\n";
       o << "  bv" << r << " = lv" << tag << "[0]; bi" << r << " = li" << tag << "[0]; bn" << r << " = ln" << tag << "[0];\n";
-      o << "  for (int w = 1; w < " << W << "; ++w) { " << ctype(in) << " ov = lv" << tag << "[w]; i64 oi = li" << tag
+      o << "  for (int w = 1; w < " << W << "; ++w) { " << ctype(in) << " ov = lv" << tag << "[w]; " << aix() << " oi = li" << tag
         << "[w]; bool on = ln" << tag << "[w]; " << comb_arg("ov", "oi", "on") << " }\n";
     } else {
       o << "  __shared__ decltype(acc" << r << ") lr" << tag << "[" << W << "];\n";
@@ -646,7 +678,8 @@ void Gen::emit_red_finish(int ni, int phase) {
   }
   // final value
   if (arg) {
-    o << "  const i64 s" << r << " = (bn" << r << " || bi" << r << " == 9223372036854775807ll) ? 0ll : bi" << r << ";\n";
+    o << "  const i64 s" << r << " = (bn" << r << " || bi" << r << " == " << aix_none() << ") ? 0ll : (i64)bi" << r
+      << ";\n";
   } else {
     std::string v = "acc" + r;
     if (dt_is_int(n.dtype)) v = std::string("(") + stype(n.dtype) + ")" + v;
@@ -673,7 +706,10 @@ std::string Gen::generate(RegionCode* rc) {
   for (auto& l : R.leaves) param(l.slot);
   for (auto& op : R.outputs) param(op.second);
   o << kDevicePrelude;
-  o << "extern \"C\" __global__ void __launch_bounds__(" << WG << ") " << entry << "(";
+  o << "extern \"C\" __global__ void __launch_bounds__(" << WG << ") ";
+  // line kernels: ask for the occupancy the cache budget was sized for (two groups per CU)
+  if (!flat && min_waves > 1) o << "__attribute__((amdgpu_waves_per_eu(" << min_waves << "))) ";
+  o << entry << "(";
   for (size_t i = 0; i < param_slots.size(); ++i) o << (i ? ", " : "") << "void* __restrict__ p" << i;
   o << ") {\n";
   int vecaxis = flat ? rank - 1 : a;
@@ -745,7 +781,12 @@ std::string Gen::generate(RegionCode* rc) {
   }
   // ---- line kernel ----
   // caches
-  for (int c : cached) o << "  " << ctype(node(c).dtype) << " cache" << c << "[" << NC << "][" << V << "];\n";
+  for (int c : cached) {
+    const RNode& cn = node(c);
+    if (packed_cache(c)) o << "  u32 cache" << c << "[" << NC << "][" << V / 2 << "];\n";
+    else o << "  " << (cn.kind == RK_LEAF ? stype(R.leaves[cn.leaf].dtype) : ctype(cn.dtype)) << " cache" << c << "["
+           << NC << "][" << V << "];\n";
+  }
   // line-level (level 0) LINE nodes
   for (size_t i = 0; i < R.nodes.size(); ++i)
     if (!full((int)i) && node((int)i).level == 0 && !is_red(node((int)i).kind)) emit_line_node((int)i);

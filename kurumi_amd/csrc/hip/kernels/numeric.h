@@ -15,12 +15,8 @@ template <int V>
 struct DTag { static constexpr int value = V; };
 
 __device__ __forceinline__ float d_bf16_ld(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
-__device__ __forceinline__ uint16_t d_bf16_st(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// v_cvt_pk_bf16_f32 (round to nearest even, NaN quieted keeping sign and top payload bits)
+__device__ __forceinline__ uint16_t d_bf16_st(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float d_f16_ld(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t d_f16_st(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
 __device__ __forceinline__ float d_e4m3_ld(uint8_t b) {

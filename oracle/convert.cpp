@@ -37,7 +37,8 @@ static uint32_t round_f64_ieee(double x, int eb, int mb) {
   uint64_t man = u & ((1ull << 52) - 1);
   uint32_t expall = (1u << eb) - 1;
   if (exp == 0x7ff) {
-    if (man) return sign | (expall << mb) | (1u << (mb - 1)) | static_cast<uint32_t>(man >> (52 - mb + 1));
+    // NaN: quiet bit set, the top mb mantissa bits kept (half 2.7.1 f64_to_f16_fallback)
+    if (man) return sign | (expall << mb) | (1u << (mb - 1)) | static_cast<uint32_t>(man >> (52 - mb));
     return sign | (expall << mb);
   }
   if (exp == 0) return sign;  // f64 subnormals are far below every target's range
@@ -69,7 +70,14 @@ static double decode_ieee(uint32_t b, int eb, int mb) {
   bool neg = (b >> (eb + mb)) & 1u;
   uint32_t e = (b >> mb) & expall, m = b & ((1u << mb) - 1);
   double v;
-  if (e == expall) v = m ? std::numeric_limits<double>::quiet_NaN() : INFINITY;
+  if (e == expall && m) {
+    // NaN keeps sign and payload, quiet bit set (half 2.7.1 f16_to_f64_fallback)
+    uint64_t bits = (static_cast<uint64_t>(neg) << 63) | 0x7ff8000000000000ull | (static_cast<uint64_t>(m) << (52 - mb));
+    double d;
+    std::memcpy(&d, &bits, 8);
+    return d;
+  }
+  if (e == expall) v = INFINITY;
   else if (e == 0) v = std::ldexp(static_cast<double>(m), 1 - bias - mb);
   else v = std::ldexp(1.0 + static_cast<double>(m) / (1u << mb), static_cast<int>(e) - bias);
   return neg ? -v : v;

@@ -10,8 +10,8 @@ import numpy as np
 import pytest
 
 from kurumi_amd import DType, Graph, Tensor
-from kutest import (assert_close, bf16_bits_to_f32, f32_to_bf16_bits, interpret, rand_range, randn, rel_err,
-                    to_f32)
+from kutest import (assert_close, bf16_bits_to_f32, cast_bits, f32_to_bf16_bits, interpret, rand_range, randn,
+                    rel_err, to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -361,3 +361,31 @@ def test_missing_feed_is_an_error(hip):
     y = g.add(x, x)
     with pytest.raises(K.KuError, match="missing feed"):
         hip.eval_with(g, y, {})
+
+
+@pytest.mark.parametrize("to", [DType.BF16, DType.F16])
+def test_f32_to_half_casts_bit_exact_across_the_bit_space(hip, to):
+    # every 257th f32 bit pattern (all exponents, signs, NaN payloads, denormals) plus the
+    # rounding ties around each half-precision step
+    pats = np.arange(0, 2 ** 32, 257, dtype=np.uint64).astype(np.uint32)
+    ties = (np.arange(0, 2 ** 16, dtype=np.uint32) << 16) | np.uint32(0x8000)
+    bits = np.concatenate([pats, ties, ties + 1, ties - 1])
+    vals = bits.view(np.float32)
+    g = Graph()
+    x = g.input([vals.size], DType.F32)
+    c = g.cast(x, to)
+    got = hip.eval_with(g, c, {x: Tensor.from_numpy(vals)}).numpy()
+    want = cast_bits(vals, DType.F32, to)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("frm", [DType.BF16, DType.F16])
+@pytest.mark.parametrize("to", [DType.F32, DType.F64, DType.I32])
+def test_half_casts_bit_exact_for_every_pattern(hip, frm, to):
+    bits = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    g = Graph()
+    x = g.input([bits.size], frm)
+    c = g.cast(x, to)
+    got = hip.eval_with(g, c, {x: Tensor(frm, [bits.size], bits.tobytes())}).numpy()
+    want = cast_bits(bits, frm, to)
+    np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))

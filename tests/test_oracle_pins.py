@@ -78,6 +78,34 @@ def test_f16_matches_numpy():
     np.testing.assert_array_equal(got, x.astype(np.float16))
 
 
+def test_nan_payloads_follow_the_half_crate():
+    # Casts go through f64 (kurumi_core/src/dtype/convert.rs:14-70) with the half crate's
+    # conversions: a NaN keeps its sign and its top mantissa bits and gets the quiet bit. For quiet
+    # NaNs that is exactly numpy's rule (npy_floatbits_to_halfbits / npy_halfbits_to_floatbits),
+    # so numpy pins the payload shift in both directions; signalling NaNs additionally get the
+    # quiet bit (0x200 in f16, 0x400000 in f32), which numpy does not add.
+    rng = np.random.default_rng(5)
+    man = rng.integers(0, 1 << 22, 4000, dtype=np.uint32)
+    sign = rng.integers(0, 2, 4000, dtype=np.uint32) << 31
+    qnan = (sign | np.uint32(0x7FC00000) | man).view(np.float32)
+    got = cast_bits(qnan, DType.F32, DType.F16)
+    np.testing.assert_array_equal(got, qnan.astype(np.float16).view(np.uint16))
+    snan = (sign | np.uint32(0x7F800000) | (man | 1)).view(np.float32)  # quiet bit clear
+    got = cast_bits(snan, DType.F32, DType.F16)
+    want = snan.astype(np.float16).view(np.uint16) | np.uint16(0x0200)
+    # numpy turns an all-zero kept payload into 1 to stay a NaN; half's quiet bit already does
+    empty = ((snan.view(np.uint32) & np.uint32(0x7FFFFF)) >> 13) == 0
+    want = np.where(empty, (sign >> 16).astype(np.uint16) | np.uint16(0x7E00), want)
+    np.testing.assert_array_equal(got, want)
+    h = (np.uint16(0x7E00) | (rng.integers(0, 1 << 9, 4000, dtype=np.uint16))) | (
+        rng.integers(0, 2, 4000, dtype=np.uint16) << 15)
+    got = cast_bits(h, DType.F16, DType.F32).view(np.uint32)
+    np.testing.assert_array_equal(got, h.view(np.float16).astype(np.float32).view(np.uint32))
+    # bf16 <-> f32: the upper half of the f32 pattern, quiet bit (0x40) forced on the way down
+    b = cast_bits(snan, DType.F32, DType.BF16)
+    np.testing.assert_array_equal(b, (snan.view(np.uint32) >> 16).astype(np.uint16) | np.uint16(0x40))
+
+
 def _e4m3_table():
     v = np.array([cast_bits(np.array([b], np.uint8), DType.F8E4M3, DType.F64)[0] for b in range(256)])
     return v
