@@ -248,7 +248,13 @@ std::string Gen::op_expr(int ni, const std::string& j) const {
       return "(" + T + ")(0 - (" + U + ")" + in(0) + ")";
     case (int)OpKind::Recip: return f64 ? "(1.0 / " + in(0) + ")" : rnd(d, "(1.0f / " + in(0) + ")");
     case (int)OpKind::Sqrt: return f64 ? "sqrt(" + in(0) + ")" : rnd(d, "sqrtf(" + in(0) + ")");
-    case (int)OpKind::Exp2: return f64 ? "exp2(" + in(0) + ")" : rnd(d, "exp2f(" + in(0) + ")");
+    case (int)OpKind::Exp2:
+      if (f64) return "exp2(" + in(0) + ")";
+      // rounded to 16 or 8 bits right away: the bare v_exp_f32 (1 ulp; results below 2^-126,
+      // which would be bf16 denormals, come out as zero) instead of the denormal-safe exp2f
+      if (d == DType::BF16 || d == DType::F16 || d == DType::F8E4M3 || d == DType::F8E5M2)
+        return rnd(d, "__builtin_amdgcn_exp2f(" + in(0) + ")");
+      return rnd(d, "exp2f(" + in(0) + ")");
     case (int)OpKind::Log2: return f64 ? "log2(" + in(0) + ")" : rnd(d, "log2f(" + in(0) + ")");
     case (int)OpKind::Sin: return f64 ? "sin(" + in(0) + ")" : rnd(d, "sinf(" + in(0) + ")");
     case (int)OpKind::Floor: return f64 ? "floor(" + in(0) + ")" : rnd(d, "floorf(" + in(0) + ")");
@@ -340,9 +346,10 @@ void Gen::plan_layout() {
   }
   // multi-level programs keep lines in registers: aim at ~8 chunks per thread;
   // single-level reductions stream: ~16 chunks per thread.
+  // ~16 chunks per thread: long lines get 256-512 threads with the line cached in registers,
+  // which leaves room for two or three groups per CU
   int target = 16;
-  for (auto& n : R.nodes)
-    if (n.level >= 2) target = 8;
+  if (const char* e = std::getenv("KURUMI_HIP_LINE_CHUNKS")) target = std::max(1, std::atoi(e));
   uint64_t t = 1;
   while (t < 1024 && t * (uint64_t)target < chunks) t *= 2;
   TPL = (int)t;
