@@ -1,0 +1,350 @@
+// MFMA GEMM with direct-to-LDS staging for gfx950 (kernel family 2):
+// C[b][m][n] = alpha * colscale[n] * sum_k A[b][m][k] * B[b][k][n], f32 accumulation, one rounding.
+//
+// Stages of 128 K-bytes go from global memory straight into LDS with global_load_lds_dwordx4
+// (lane l of a wave writes bytes 16l..16l+15 of the wave's 1 KB destination), double-buffered
+// with one barrier per stage, so no registers or VALU work are spent on staging. Because the LDS
+// position of every 16-byte chunk is fixed by the lane, the bank-conflict-avoiding layout is
+// chosen on the global side: each lane fetches the chunk that belongs at its swizzled position.
+//   A, and B when k-contiguous ("NT"): rows of 128 B, chunk c of row r stored at c ^ (r % 8), so
+//     the 32 rows a fragment read touches spread over all banks.
+//   B when n-contiguous ("NN", [k][n] row-major): rows of BN*2 bytes kept n-major, 16-byte chunk c
+//     of k-row r stored at c ^ 4(r % 4); fragments are read with ds_read_b64_tr_b16, which hands
+//     each lane 4 consecutive k values of one column (two reads make the 8 a bf16 MFMA takes).
+// bf16/f16 use v_mfma_f32_32x32x16_{bf16,f16}; OCP e4m3 uses v_mfma_f32_32x32x64_f8f6f4 (NT).
+// Rows and columns past M and N are clamped on load (their results are never stored), so every
+// load is in bounds. Work-groups are remapped so the tiles resident on one XCD share A rows and
+// B columns in its L2. Semantics: kurumi_core/src/interp/contract.rs:26-64.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdlib>
+#include <string>
+
+#include "kernels.h"
+#include "numeric.h"
+
+namespace ku::hipbk {
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
+#define KU_LDS __attribute__((address_space(3)))
+
+enum Elem : int { E_BF16 = 0, E_F16 = 1, E_FP8 = 2 };
+
+constexpr int KB = 128;  // K bytes per stage (one row of an A/B^T stage)
+
+template <int E>
+struct Op;
+template <>
+struct Op<E_BF16> {
+  static constexpr int KSTEP = 32;  // K bytes per MFMA (16 bf16)
+  static constexpr int LV = 1;      // 16-byte pieces per lane per operand
+  __device__ static void run(f32x16& c, const u32x4* a, const u32x4* b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a[0]), __builtin_bit_cast(bf16x8, b[0]), c,
+                                                0, 0, 0);
+  }
+};
+template <>
+struct Op<E_F16> {
+  static constexpr int KSTEP = 32;
+  static constexpr int LV = 1;
+  __device__ static void run(f32x16& c, const u32x4* a, const u32x4* b) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a[0]), __builtin_bit_cast(f16x8, b[0]), c, 0,
+                                               0, 0);
+  }
+};
+template <>
+struct Op<E_FP8> {
+  static constexpr int KSTEP = 64;  // 64 e4m3 per MFMA
+  static constexpr int LV = 2;
+  __device__ static void run(f32x16& c, const u32x4* a, const u32x4* b) {
+    i32x8 av, bv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      av[i] = (int)a[0][i];
+      av[4 + i] = (int)a[1][i];
+      bv[i] = (int)b[0][i];
+      bv[4 + i] = (int)b[1][i];
+    }
+    // format 0 = e4m3 for both operands; zero scales select the unscaled instruction
+    c = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 0, 0, 0, 0, 0, 0);
+  }
+};
+
+template <int OT>
+__device__ __forceinline__ void store_out(void* c, int64_t idx, float v) {
+  if constexpr (OT == GT_BF16) static_cast<uint16_t*>(c)[idx] = d_bf16_st(v);
+  else if constexpr (OT == GT_F16) static_cast<uint16_t*>(c)[idx] = d_f16_st(v);
+  else static_cast<float*>(c)[idx] = v;
+}
+
+// consecutive ids go to XCD id % 8: regroup them into contiguous ranges per XCD, then walk tiles
+// in groups of GM tile-rows so the tiles running together reuse A rows and B columns
+__device__ __forceinline__ void tile_of(int pid, int tm, int tn, int* im, int* in) {
+  const int total = tm * tn;
+  const int per = total / 8;
+  if (pid < per * 8) pid = (pid % 8) * per + pid / 8;
+  constexpr int GM = 8;
+  const int group = pid / (GM * tn);
+  const int first = group * GM;
+  const int gs = min(tm - first, GM);
+  const int r = pid % (GM * tn);
+  *im = first + r % gs;
+  *in = r / gs;
+}
+
+__device__ __forceinline__ void dma16(const void* g, KU_LDS unsigned char* l) {
+  __builtin_amdgcn_global_load_lds(g, (KU_LDS void*)l, 16, 0, 0);
+}
+
+template <int E, bool BNMAJ, int OT, int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(WM* WN * 64)
+    __attribute__((amdgpu_waves_per_eu((WM * WN + 3) / 4, (WM * WN + 3) / 4))) gemm_lds_k(GemmArgs a) {
+  constexpr int NW = WM * WN, NT = NW * 64;
+  constexpr int EB = (E == E_FP8) ? 1 : 2;
+  constexpr int KE = KB / EB;  // K elements per stage
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int KSTEP = Op<E>::KSTEP, LV = Op<E>::LV, NKS = KB / KSTEP;
+  constexpr int ABYTES = BM * KB, BBYTES = BN * KB;  // NN: KE rows of BN*2 bytes, the same size
+  constexpr int AI = ABYTES / 1024 / NW;             // 1 KB DMA blocks per wave per stage
+  constexpr int BI = BBYTES / 1024 / NW;
+  constexpr int NROW = BN * 2;         // NN: bytes per k-row
+  constexpr int NCH = NROW / 16;       // NN: 16-byte chunks per k-row
+  constexpr int NRPB = 1024 / NROW;    // NN: k-rows per 1 KB block
+  static_assert(AI * NW * 1024 == ABYTES && BI * NW * 1024 == BBYTES, "stage / wave mismatch");
+  static_assert(!BNMAJ || (E != E_FP8 && NCH >= 16 && NRPB >= 1 && NRPB * NROW == 1024), "NN layout");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[2 * (ABYTES + BBYTES)];
+  KU_LDS unsigned char* lds = (KU_LDS unsigned char*)lds_raw;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  const int wm = wave / WN, wn = wave % WN;
+  const int tm = (int)((a.m + BM - 1) / BM), tn = (int)((a.n + BN - 1) / BN);
+  int im, in;
+  tile_of(blockIdx.x, tm, tn, &im, &in);
+  const int64_t m0 = (int64_t)im * BM, n0 = (int64_t)in * BN;
+  const int64_t bz = blockIdx.y;
+  const unsigned char* A = static_cast<const unsigned char*>(a.a) + bz * a.sab * EB;
+  const unsigned char* B = static_cast<const unsigned char*>(a.b) + bz * a.sbb * EB;
+  const int KT = (int)(a.k / KE);
+
+  // per-lane global sources of this lane's DMA chunks (stage 0; later stages add kt * stride)
+  const unsigned char* asrc[AI];
+#pragma unroll
+  for (int i = 0; i < AI; ++i) {
+    const int blk = i * NW + wave, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+    const int64_t gm = m0 + r < a.m ? m0 + r : a.m - 1;
+    asrc[i] = A + gm * a.sam * EB + c * 16;
+  }
+  const unsigned char* bsrc[BI];
+  int64_t bstep;  // bytes between consecutive stages
+  if constexpr (!BNMAJ) {
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+      const int blk = i * NW + wave, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+      const int64_t gn = n0 + r < a.n ? n0 + r : a.n - 1;
+      bsrc[i] = B + gn * a.sbn * EB + c * 16;
+    }
+    bstep = KB;
+  } else {
+#pragma unroll
+    for (int i = 0; i < BI; ++i) {
+      const int blk = i * NW + wave, r = blk * NRPB + lane / NCH, c = (lane % NCH) ^ (4 * (r & 3));
+      const int64_t gn = n0 + c * 8 < a.n ? n0 + c * 8 : a.n - 8;
+      bsrc[i] = B + ((int64_t)r * a.sbk + gn) * 2;
+    }
+    bstep = (int64_t)KE * a.sbk * 2;
+  }
+  auto issue = [&](int kt, int buf) {
+    KU_LDS unsigned char* L = lds + buf * (ABYTES + BBYTES);
+#pragma unroll
+    for (int i = 0; i < AI; ++i) dma16(asrc[i] + (int64_t)kt * KB, L + (i * NW + wave) * 1024);
+#pragma unroll
+    for (int i = 0; i < BI; ++i) dma16(bsrc[i] + (int64_t)kt * bstep, L + ABYTES + (i * NW + wave) * 1024);
+  };
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // fragment reads from one stage
+  auto afrags = [&](const KU_LDS unsigned char* L, int ks, u32x4 (&fa)[FM][LV]) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int r = wm * TM + i * 32 + l32;
+#pragma unroll
+      for (int v = 0; v < LV; ++v) {
+        const int c = ks * (KSTEP / 16) + h * LV + v;
+        fa[i][v] = *(const KU_LDS u32x4*)(L + r * KB + ((c ^ (r & 7)) << 4));
+      }
+    }
+  };
+  auto bfrags_nt = [&](const KU_LDS unsigned char* L, int ks, u32x4 (&fb)[FN][LV]) {
+    const KU_LDS unsigned char* LB = L + ABYTES;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int r = wn * TN + j * 32 + l32;
+#pragma unroll
+      for (int v = 0; v < LV; ++v) {
+        const int c = ks * (KSTEP / 16) + h * LV + v;
+        fb[j][v] = *(const KU_LDS u32x4*)(LB + r * KB + ((c ^ (r & 7)) << 4));
+      }
+    }
+  };
+  // NN: ds_read_b64_tr_b16 -- in each 16-lane group, input lane 4k'+q points at k-row k',
+  // columns 4q..4q+3, and output lane i then holds rows 0..3 of column i
+  auto bfrag_nn = [&](const KU_LDS unsigned char* L, int ks, int j) {
+    const KU_LDS unsigned char* LB = L + ABYTES;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int n = wn * TN + j * 32 + (g & 1) * 16 + (c16 & 3) * 4;
+    u32x2 half[2];
+#pragma unroll
+    for (int r2 = 0; r2 < 2; ++r2) {
+      const int k = ks * 16 + (g >> 1) * 8 + r2 * 4 + (c16 >> 2);
+      const KU_LDS unsigned char* p = LB + k * NROW + (((n >> 3) ^ (4 * (k & 3))) << 4) + (n & 7) * 2;
+      half[r2] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KU_LDS s16x4*)p));
+    }
+    return u32x4{half[0][0], half[0][1], half[1][0], half[1][1]};
+  };
+
+  if (KT > 0) issue(0, 0);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    const KU_LDS unsigned char* L = lds + cur * (ABYTES + BBYTES);
+    if constexpr (BNMAJ) {
+      // The transposing reads are not known to the compiler to miss the buffer the next stage's
+      // DMA fills, so they all go ahead of that DMA (a later one would wait for it).
+      u32x4 bst[NKS][FN];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bst[ks][j] = bfrag_nn(L, ks, j);
+      if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
+      u32x4 af[2][FM][LV];
+      afrags(L, 0, af[0]);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        if (ks + 1 < NKS) afrags(L, ks + 1, af[(ks + 1) & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) Op<E>::run(acc[i][j], af[ks & 1][i], &bst[ks][j]);
+      }
+    } else {
+      if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
+      // fragments double-buffered across k-steps: step ks+1's LDS reads run under step ks's MFMAs
+      u32x4 af[2][FM][LV], bfr[2][FN][LV];
+      afrags(L, 0, af[0]);
+      bfrags_nt(L, 0, bfr[0]);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        if (ks + 1 < NKS) {
+          afrags(L, ks + 1, af[(ks + 1) & 1]);
+          bfrags_nt(L, ks + 1, bfr[(ks + 1) & 1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) Op<E>::run(acc[i][j], af[ks & 1][i], bfr[ks & 1][j]);
+      }
+    }
+    // this thread's DMA for stage kt+1 has landed; the barrier publishes it and retires stage kt
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  }
+
+  // epilogue: lane owns column l32 and rows 8*(v/4) + 4*h + v%4 of each 32x32 tile
+  const float alpha = a.alpha ? a.alpha[0] : 1.f;
+  void* C = static_cast<unsigned char*>(a.c) + bz * a.m * a.n * (OT == GT_F32 ? 4 : 2);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * TN + j * 32 + l32;
+    if (col >= a.n) continue;
+    const float cs = a.col_scale ? alpha * a.col_scale[col * a.col_scale_stride] : alpha;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t row = m0 + wm * TM + i * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
+        if (row < a.m) store_out<OT>(C, row * a.n + col, acc[i][j][v] * cs);
+      }
+    }
+  }
+}
+
+template <int E, bool BNMAJ, int OT, int BM, int BN, int WM, int WN>
+void launch_tile(const GemmArgs& a, hipStream_t s) {
+  const int tm = (int)((a.m + BM - 1) / BM), tn = (int)((a.n + BN - 1) / BN);
+  dim3 grid((unsigned)(tm * tn), (unsigned)a.batch);
+  hipLaunchKernelGGL((gemm_lds_k<E, BNMAJ, OT, BM, BN, WM, WN>), grid, dim3(WM * WN * 64), 0, s, a);
+}
+
+template <int E, bool BNMAJ, int OT>
+void launch_cfg(const GemmArgs& a, hipStream_t s) {
+  launch_tile<E, BNMAJ, OT, 256, 256, 2, 4>(a, s);
+}
+
+template <int E, bool BNMAJ>
+void launch_e(const GemmArgs& a, hipStream_t s) {
+  switch (a.out_type) {
+    case GT_BF16: launch_cfg<E, BNMAJ, GT_BF16>(a, s); return;
+    case GT_F16: launch_cfg<E, BNMAJ, GT_F16>(a, s); return;
+    default: launch_cfg<E, BNMAJ, GT_F32>(a, s); return;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+bool gemm_lds_ok(const GemmArgs& a) {
+  if (const char* e = std::getenv("KURUMI_HIP_NO_MFMA"); e && *e && *e != '0') return false;
+  if (const char* e = std::getenv("KURUMI_HIP_GEMM_V1"); e && *e && *e != '0') return false;
+  const bool fp8 = a.in_type == GT_F8E4M3;
+  if (!(a.in_type == GT_BF16 || a.in_type == GT_F16 || fp8)) return false;
+  if (!(a.out_type == GT_BF16 || a.out_type == GT_F16 || a.out_type == GT_F32)) return false;
+  const int64_t ke = fp8 ? 128 : 64, eb = fp8 ? 1 : 2, vec = 16 / eb;
+  if (a.k % ke != 0 || a.k == 0 || a.m == 0 || a.n == 0) return false;
+  if (a.sak != 1 || (a.m > 1 && a.sam % vec) || a.sab % vec) return false;
+  const bool nt = a.sbk == 1, nn = a.sbn == 1 && !fp8;
+  if (nt) {
+    if ((a.n > 1 && a.sbn % vec) || a.sbb % vec) return false;
+  } else if (nn) {
+    if (a.sbk % vec || a.n % 8 || a.sbb % vec) return false;
+  } else {
+    return false;
+  }
+  if (a.a && (!aligned16(a.a) || !aligned16(a.b))) return false;
+  return a.batch <= 65535;
+}
+
+void launch_gemm_lds(const GemmArgs& a, hipStream_t s) {
+  const bool nt = a.sbk == 1;
+  if (a.in_type == GT_F8E4M3) {
+    launch_e<E_FP8, false>(a, s);
+  } else if (a.in_type == GT_F16) {
+    if (nt) launch_e<E_F16, false>(a, s);
+    else launch_e<E_F16, true>(a, s);
+  } else {
+    if (nt) launch_e<E_BF16, false>(a, s);
+    else launch_e<E_BF16, true>(a, s);
+  }
+}
+
+}  // namespace ku::hipbk

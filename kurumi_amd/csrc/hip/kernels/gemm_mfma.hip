@@ -96,7 +96,8 @@ __device__ __forceinline__ void tile_of(int pid, int tm, int tn, int* im, int* i
 }
 
 template <int E, bool BNMAJ, int OT, int BM, int BN, int WM, int WN>
-__global__ void __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_eu(1, 1))) gemm_mfma_k(GemmArgs a) {
+__global__ void __launch_bounds__(WM* WN * 64)
+    __attribute__((amdgpu_waves_per_eu((WM * WN + 3) / 4, (WM * WN + 3) / 4))) gemm_mfma_k(GemmArgs a) {
   constexpr int NT = WM * WN * 64;
   constexpr int EB = (E == E_FP8) ? 1 : 2;
   constexpr int KE = KB / EB;  // K elements per stage
@@ -141,7 +142,7 @@ __global__ void __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_e
                            : u32x4{0, 0, 0, 0};
       }
     } else {
-      const int nc = tid % (BN / 8), kq = tid / (BN / 8);
+      const int kq = tid % (KE / R), nc = tid / (KE / R);
       const int64_t gn = n0 + nc * 8;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
@@ -165,8 +166,9 @@ __global__ void __launch_bounds__(WM* WN * 64) __attribute__((amdgpu_waves_per_e
         *reinterpret_cast<u32x4*>(LBp + row * LDS_ROW + col * 16) = rb[i];
       }
     } else {
-      // R k-rows x 8 n-columns of 16-bit values -> 8 n-rows x R k-values
-      const int nc = tid % (BN / 8), kq = tid / (BN / 8);
+      // R k-rows x 8 n-columns of 16-bit values -> 8 n-rows x R k-values; consecutive lanes take
+      // consecutive k groups of one n chunk, so the 16 lanes of a write cover 64 distinct banks
+      const int kq = tid % (KE / R), nc = tid / (KE / R);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int w = j >> 1, hi = (j & 1) * 16;
@@ -267,6 +269,7 @@ int tile_choice() {
     if (v == "256x128") return 0;
     if (v == "128x128") return 2;
     if (v == "128x256") return 3;
+    if (v == "256x256w8") return 4;
     return 1;
   }();
   return t;
@@ -278,6 +281,7 @@ void launch_cfg(const GemmArgs& a, hipStream_t s) {
     case 1: launch_tile<E, BNMAJ, OT, 256, 256, 2, 2>(a, s); return;
     case 2: launch_tile<E, BNMAJ, OT, 128, 128, 2, 2>(a, s); return;
     case 3: launch_tile<E, BNMAJ, OT, 128, 256, 2, 2>(a, s); return;
+    case 4: launch_tile<E, BNMAJ, OT, 256, 256, 2, 4>(a, s); return;
     default: launch_tile<E, BNMAJ, OT, 256, 128, 2, 2>(a, s); return;
   }
 }

@@ -20,6 +20,10 @@ def bf16_tensor(x: np.ndarray) -> Tensor:
     return Tensor(DType.BF16, x.shape, f32_to_bf16_bits(x).tobytes())
 
 
+def f16_tensor(x: np.ndarray) -> Tensor:
+    return Tensor(DType.F16, x.shape, x.astype(np.float16).tobytes())
+
+
 # ---------------- config 1: fused elementwise + reduce ----------------
 
 def cfg1_graph(n: int, m: int):
@@ -145,6 +149,25 @@ def test_cfg3_bf16_gemm_matches_oracle(hip, m, k, n):
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="gemm vs oracle")
 
 
+@pytest.mark.parametrize("dt", [DType.BF16, DType.F16])
+@pytest.mark.parametrize("nt", [False, True])
+@pytest.mark.parametrize("m,k,n", [(300, 192, 520), (256, 128, 256), (1, 64, 8), (513, 320, 264)])
+def test_gemm_layouts_and_edges_match_oracle(hip, dt, nt, m, k, n):
+    # NN ([k][n] rhs) and NT ([n][k] rhs, the linear-layer layout), tiles cut by M and N
+    print(f"gemm {dt.name} nt={nt} {m}x{k}x{n}", flush=True)
+    g = Graph()
+    a = g.input([m, k], dt)
+    b = g.input([n, k] if nt else [k, n], dt)
+    c = g.dot_general(a, b, [1], [1] if nt else [0])
+    av = randn([m, k], 35, 1.0 / 16)
+    bv = randn([n, k] if nt else [k, n], 36, 1.0 / 16)
+    mk = f16_tensor if dt == DType.F16 else bf16_tensor
+    feeds = {a: mk(av), b: mk(bv)}
+    got = to_f32(hip.eval_with(g, c, feeds))
+    want = to_f32(interpret(g, [c], feeds)[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="gemm layout")
+
+
 def test_cfg3_batched_gemm_matches_oracle(hip):
     g = Graph()
     a = g.input([4, 256, 128], DType.BF16)
@@ -159,10 +182,6 @@ def test_cfg3_batched_gemm_matches_oracle(hip):
 
 
 # ---------------- config 4: causal attention ----------------
-
-def f16_tensor(x: np.ndarray) -> Tensor:
-    return Tensor(DType.F16, x.shape, x.astype(np.float16).tobytes())
-
 
 def attention_graph(shape, dt, causal, fused):
     g = Graph()
