@@ -11,6 +11,9 @@
 //   B when n-contiguous ("NN", [k][n] row-major): rows of BN*2 bytes kept n-major, 16-byte chunk c
 //     of k-row r stored at c ^ 4(r % 4); fragments are read with ds_read_b64_tr_b16, which hands
 //     each lane 4 consecutive k values of one column (two reads make the 8 a bf16 MFMA takes).
+// The MFMAs produce C^T tiles (B fragment as the A operand) so that each lane ends up with runs
+// of 4 consecutive output columns; the epilogue parks them in LDS and writes whole 128-byte row
+// segments.
 // bf16/f16 use v_mfma_f32_32x32x16_{bf16,f16}; OCP e4m3 uses v_mfma_f32_32x32x64_f8f6f4 (NT).
 // Rows and columns past M and N are clamped on load (their results are never stored), so every
 // load is in bounds. Work-groups are remapped so the tiles resident on one XCD share A rows and
@@ -243,7 +246,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-          for (int j = 0; j < FN; ++j) Op<E>::run(acc[i][j], af[ks & 1][i], &bst[ks][j]);
+          for (int j = 0; j < FN; ++j) Op<E>::run(acc[i][j], &bst[ks][j], af[ks & 1][i]);
       }
     } else {
       if (kt + 1 < KT) issue(kt + 1, cur ^ 1);
@@ -261,7 +264,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
 #pragma unroll
         for (int i = 0; i < FM; ++i)
 #pragma unroll
-          for (int j = 0; j < FN; ++j) Op<E>::run(acc[i][j], af[ks & 1][i], bfr[ks & 1][j]);
+          for (int j = 0; j < FN; ++j) Op<E>::run(acc[i][j], bfr[ks & 1][j], af[ks & 1][i]);
       }
     }
     // this thread's DMA for stage kt+1 has landed; the barrier publishes it and retires stage kt
@@ -269,21 +272,87 @@ __global__ void __launch_bounds__(WM* WN * 64)
     __syncthreads();
   }
 
-  // epilogue: lane owns column l32 and rows 8*(v/4) + 4*h + v%4 of each 32x32 tile
+  // Epilogue. The MFMAs computed C^T tiles (B fragment as the A operand): lane l32 owns row
+  // i*32 + l32 of the wave's TM x TN block and, in register group g of tile j, the 4 columns
+  // j*32 + 8g + 4h + 0..3. Scaled values are rounded, parked in LDS (the stage buffers are free
+  // after the loop's last barrier) and written back row-contiguous, 16 bytes per lane and 128
+  // bytes per row and instruction.
   const float alpha = a.alpha ? a.alpha[0] : 1.f;
   void* C = static_cast<unsigned char*>(a.c) + bz * a.m * a.n * (OT == GT_F32 ? 4 : 2);
+  const int64_t rbase = m0 + wm * TM, cbase = n0 + wn * TN;
+  float cs[FN][4][4];  // column scales of this lane's columns
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int64_t col = n0 + wn * TN + j * 32 + l32;
-    if (col >= a.n) continue;
-    const float cs = a.col_scale ? alpha * a.col_scale[col * a.col_scale_stride] : alpha;
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t col = cbase + j * 32 + g * 8 + h * 4 + e;
+        cs[j][g][e] = a.col_scale ? alpha * a.col_scale[(col < a.n ? col : a.n - 1) * a.col_scale_stride] : alpha;
+      }
+  if constexpr (OT != GT_F32) {
+    constexpr int ROWB = TN * 2;          // bytes per staged row
+    constexpr int UPR = ROWB / 8;         // 8-byte units per row
+    static_assert(UPR == 16 && TM * ROWB * NW <= 2 * (ABYTES + BBYTES), "epilogue staging");
+    KU_LDS unsigned char* EP = lds + wave * TM * ROWB;
+    // unit u of row r sits at u ^ ((r / 2) % 16): the 32 rows one write touches cover all banks
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
+      const int r = i * 32 + l32;
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t row = m0 + wm * TM + i * 32 + (v >> 2) * 8 + h * 4 + (v & 3);
-        if (row < a.m) store_out<OT>(C, row * a.n + col, acc[i][j][v] * cs);
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int u = j * 8 + g * 2 + h;
+          u32x2 w;
+          if constexpr (OT == GT_BF16) {
+            w[0] = (uint32_t)d_bf16_st(acc[i][j][4 * g] * cs[j][g][0]) |
+                   ((uint32_t)d_bf16_st(acc[i][j][4 * g + 1] * cs[j][g][1]) << 16);
+            w[1] = (uint32_t)d_bf16_st(acc[i][j][4 * g + 2] * cs[j][g][2]) |
+                   ((uint32_t)d_bf16_st(acc[i][j][4 * g + 3] * cs[j][g][3]) << 16);
+          } else {
+            w[0] = (uint32_t)d_f16_st(acc[i][j][4 * g] * cs[j][g][0]) |
+                   ((uint32_t)d_f16_st(acc[i][j][4 * g + 1] * cs[j][g][1]) << 16);
+            w[1] = (uint32_t)d_f16_st(acc[i][j][4 * g + 2] * cs[j][g][2]) |
+                   ((uint32_t)d_f16_st(acc[i][j][4 * g + 3] * cs[j][g][3]) << 16);
+          }
+          *(KU_LDS u32x2*)(EP + r * ROWB + ((u ^ ((r >> 1) & 15)) << 3)) = w;
+        }
+    }
+    // each wave reads back only its own block: no barrier needed beyond the LDS wait
+    const bool vec8 = (a.n & 7) == 0;
+#pragma unroll
+    for (int q = 0; q < TM / 8; ++q) {
+      const int r = q * 8 + (lane >> 3), c = lane & 7;
+      const int sw = (r >> 1) & 15;
+      const u32x2 lo = *(const KU_LDS u32x2*)(EP + r * ROWB + (((2 * c) ^ sw) << 3));
+      const u32x2 hi = *(const KU_LDS u32x2*)(EP + r * ROWB + (((2 * c + 1) ^ sw) << 3));
+      const int64_t row = rbase + r, col = cbase + c * 8;
+      if (row >= a.m || col >= a.n) continue;
+      uint16_t* dst = static_cast<uint16_t*>(C) + row * a.n + col;
+      if (vec8 && col + 8 <= a.n) {
+        *reinterpret_cast<u32x4*>(dst) = u32x4{lo[0], lo[1], hi[0], hi[1]};
+      } else {
+        const uint32_t w4[4] = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (col + e < a.n) dst[e] = (uint16_t)(w4[e >> 1] >> ((e & 1) * 16));
       }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int64_t row = rbase + i * 32 + l32;
+      if (row >= a.m) continue;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t col = cbase + j * 32 + g * 8 + h * 4;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col + e < a.n) static_cast<float*>(C)[row * a.n + col + e] = acc[i][j][4 * g + e] * cs[j][g][e];
+        }
     }
   }
 }
