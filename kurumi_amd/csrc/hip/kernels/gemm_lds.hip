@@ -6,8 +6,8 @@
 // with one barrier per stage, so no registers or VALU work are spent on staging. Because the LDS
 // position of every 16-byte chunk is fixed by the lane, the bank-conflict-avoiding layout is
 // chosen on the global side: each lane fetches the chunk that belongs at its swizzled position.
-//   A, and B when k-contiguous ("NT"): rows of 128 B, chunk c of row r stored at c ^ (r % 8), so
-//     the 32 rows a fragment read touches spread over all banks.
+//   A, and B when k-contiguous ("NT"): rows of 128 B, chunk c of row r stored at c ^ ((r / 2) % 8),
+//     so any 16 consecutive rows read at one logical chunk hit 16 distinct 16-byte bank groups.
 //   B when n-contiguous ("NN", [k][n] row-major): rows of BN*2 bytes kept n-major, 16-byte chunk c
 //     of k-row r stored at c ^ 4(r % 4); fragments are read with ds_read_b64_tr_b16, which hands
 //     each lane 4 consecutive k values of one column (two reads make the 8 a bf16 MFMA takes).
@@ -143,7 +143,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
   const unsigned char* asrc[AI];
 #pragma unroll
   for (int i = 0; i < AI; ++i) {
-    const int blk = i * NW + wave, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+    const int blk = i * NW + wave, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
     const int64_t gm = m0 + r < a.m ? m0 + r : a.m - 1;
     asrc[i] = A + gm * a.sam * EB + c * 16;
   }
@@ -152,7 +152,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
   if constexpr (!BNMAJ) {
 #pragma unroll
     for (int i = 0; i < BI; ++i) {
-      const int blk = i * NW + wave, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ (r & 7);
+      const int blk = i * NW + wave, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
       const int64_t gn = n0 + r < a.n ? n0 + r : a.n - 1;
       bsrc[i] = B + gn * a.sbn * EB + c * 16;
     }
@@ -190,7 +190,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
 #pragma unroll
       for (int v = 0; v < LV; ++v) {
         const int c = ks * (KSTEP / 16) + h * LV + v;
-        fa[i][v] = *(const KU_LDS u32x4*)(L + r * KB + ((c ^ (r & 7)) << 4));
+        fa[i][v] = *(const KU_LDS u32x4*)(L + r * KB + ((c ^ ((r >> 1) & 7)) << 4));
       }
     }
   };
@@ -202,7 +202,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
 #pragma unroll
       for (int v = 0; v < LV; ++v) {
         const int c = ks * (KSTEP / 16) + h * LV + v;
-        fb[j][v] = *(const KU_LDS u32x4*)(LB + r * KB + ((c ^ (r & 7)) << 4));
+        fb[j][v] = *(const KU_LDS u32x4*)(LB + r * KB + ((c ^ ((r >> 1) & 7)) << 4));
       }
     }
   };
