@@ -40,6 +40,8 @@ typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
+#define KU_LDS __attribute__((address_space(3)))
 
 constexpr int BK = 64;  // keys per block
 constexpr float LOG2E = 1.4426950408889634f;
@@ -83,7 +85,6 @@ __device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
 
-__device__ __forceinline__ int key_slot(int k) { return (k & ~12) | ((k & 4) << 1) | ((k & 8) >> 1); }
 
 // Lazy rescaling: the running max m (kept pre-multiplied by scale*log2 e) only moves when a
 // block's max exceeds it by more than RESCALE (log2 units), so most blocks skip the O rescale.
@@ -105,21 +106,21 @@ constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_DSR = 0x100, SG_DSW = 0x200;
 template <int D, int DT, int NW, int QT>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 2 : 1, QT == 1 ? 2 : 1)))
 attn_mfma_k(AttnArgs a) {
-  constexpr int NT = NW * 64, QW = 32 * QT, BQ = QW * NW;
-  constexpr int KROW = D * 2 + 16;   // LDS bytes per K row (padded)
-  constexpr int VROW = BK * 2 + 16;  // LDS bytes per V^T row (padded)
-  constexpr int KBYTES = BK * KROW, VBYTES = D * VROW;
-  constexpr int KC = BK * D / 8 / NT;  // 16-byte K chunks per thread
-  constexpr int R = BK * D / 8 / NT;   // consecutive keys per thread in the V transpose
-  constexpr int DS = D / 16;           // k-steps of S^T
-  constexpr int DTL = D / 32;          // 32-row tiles of O^T
-  static_assert(KC >= 1 && KC * NT * 8 == BK * D, "K staging");
-  static_assert(R >= 1 && R <= 4 && (R & (R - 1)) == 0 && R * NT * 8 == BK * D, "V staging");
+  constexpr int QW = 32 * QT, BQ = QW * NW;
+  constexpr int RB = D * 2;              // bytes per K / V row in LDS (no padding: swizzled)
+  constexpr int W = 256 / RB;            // rows per 256-byte bank window (64 banks)
+  constexpr int CPR = RB / 16;           // 16-byte chunks per row
+  constexpr int TBYTES = BK * RB;        // one K or V block
+  constexpr int NBLK = TBYTES / 1024 / NW;  // 1 KB DMA blocks per wave per tile
+  constexpr int DS = D / 16;             // k-steps of S^T
+  constexpr int DTL = D / 32;            // 32-row tiles of O^T
+  static_assert(W >= 1 && NBLK * NW * 1024 == TBYTES, "K / V staging");
   // every block a wave needs starts at or before the wave's first query, so a lane is never
   // fully masked in a block it needs
   static_assert(BK % 32 == 0 && (QW % BK == 0 || BK % QW == 0), "block / wave alignment");
-  __shared__ __attribute__((aligned(16))) unsigned char ldsk[2][KBYTES];
-  __shared__ __attribute__((aligned(16))) unsigned char ldsv[2][VBYTES];
+  // K buffers 0, 1 then V buffers 0, 1
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[4 * TBYTES];
+  KU_LDS unsigned char* lds = (KU_LDS unsigned char*)lds_raw;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, qc = lane & 31;
   const int64_t S = a.s;
@@ -150,53 +151,30 @@ attn_mfma_k(AttnArgs a) {
   const int64_t kend = a.causal ? (q0 + BQ < S ? q0 + BQ : S) : S;  // keys this tile needs
   const int nkb = (int)((kend + BK - 1) / BK);
 
-  u32x4 rk[KC], rv[R];
-  // V staging: lanes with consecutive ids take consecutive key groups of one 8-dim chunk, so the
-  // transposed LDS writes of a 16-lane group fill one V^T row without bank conflicts
-  const int dc = tid / (BK / R), kq = tid % (BK / R);
-  // a block past nkb loads from offset hb (zeros) instead of branching
-  auto loadK = [&](int kb) {
-    const uint32_t k0b = kb < nkb ? (uint32_t)kb * BK * D * 2 : hb;
+  // K and V blocks go global -> LDS by DMA (buffer_load ... lds: lane l of a wave writes bytes
+  // 16l..16l+15 of the wave's 1 KB destination; offsets past the head read as zeros). The LDS
+  // position of each chunk is fixed by the lane, so the swizzles are applied by choosing which
+  // global chunk each lane fetches:
+  //   K: chunk c of row r at c ^ ((r / W) % (16 / W)) -- the 16 rows one fragment read touches at
+  //      one chunk land on 16 distinct bank groups;
+  //   V: chunk c of row r at c ^ 4((r / W) % (4 / W)) -- the 4 rows x 4 chunks one transposing
+  //      read touches do.
+  auto kswz = [](int r) { return (r / W) % (16 / W); };
+  auto vswz = [](int r) { return 4 * ((r / W) % (4 / W)); };
+  auto dma = [&](__amdgpu_buffer_rsrc_t src, int kb, KU_LDS unsigned char* dst, bool isv) {
+    const uint32_t k0b = kb < nkb ? (uint32_t)kb * BK * RB : hb;
 #pragma unroll
-    for (int i = 0; i < KC; ++i) {
-      const int c = tid + i * NT, row = c / (D / 8), col = c % (D / 8);
-      rk[i] = bload(K, k0b + row * D * 2 + col * 16);
+    for (int i = 0; i < NBLK; ++i) {
+      const int blk = i * NW + wave, r = blk * (1024 / RB) + lane / CPR, pc = lane % CPR;
+      const int cc = pc ^ (isv ? vswz(r) : kswz(r));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (KU_LDS void*)(dst + blk * 1024), 16,
+                                               (int)(k0b + r * RB + cc * 16), 0, 0, 0);
     }
   };
-  auto loadV = [&](int kb) {
-    const uint32_t k0b = kb < nkb ? (uint32_t)kb * BK * D * 2 : hb;
-#pragma unroll
-    for (int r = 0; r < R; ++r) rv[r] = bload(V, k0b + (kq * R + r) * D * 2 + dc * 16);
-  };
-  auto storeK = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < KC; ++i) {
-      const int c = tid + i * NT, row = c / (D / 8), col = c % (D / 8);
-      *reinterpret_cast<u32x4*>(ldsk[buf] + row * KROW + col * 16) = rk[i];
-    }
-  };
-  // R keys x 8 dims -> 8 V^T rows x R key slots (R keys starting at a multiple of R stay
-  // contiguous under the slot permutation because R <= 4)
-  auto storeV = [&](int buf) {
-    const int slot = (kq * R & ~15) | key_slot((kq * R) & 15);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      // dims 2w (low halves) or 2w+1 (high halves) of R consecutive keys, paired by v_perm_b32
-      const int w = j >> 1;
-      const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
-      unsigned char* dst = ldsv[buf] + (dc * 8 + j) * VROW + slot * 2;
-      if constexpr (R == 4) {
-        *reinterpret_cast<u32x2*>(dst) =
-            u32x2{__builtin_amdgcn_perm(rv[1][w], rv[0][w], sel), __builtin_amdgcn_perm(rv[3][w], rv[2][w], sel)};
-      } else if constexpr (R == 2) {
-        *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(rv[1][w], rv[0][w], sel);
-      } else {
-        *reinterpret_cast<uint16_t*>(dst) = (uint16_t)((rv[0][w] >> ((j & 1) * 16)) & 0xffffu);
-      }
-    }
-  };
+  auto kbuf = [&](int i) { return lds + i * TBYTES; };
+  auto vbuf = [&](int i) { return lds + (2 + i) * TBYTES; };
   // S^T of one block from a K buffer: 2 key tiles x QT query tiles, DS k-steps
-  auto s_mfma = [&](const unsigned char* L, f32x16 (&sc)[QT][2]) {
+  auto s_mfma = [&](const KU_LDS unsigned char* L, f32x16 (&sc)[QT][2]) {
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -207,7 +185,8 @@ attn_mfma_k(AttnArgs a) {
     for (int s = 0; s < DS; ++s)
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(L + (t * 32 + qc) * KROW + s * 32 + h * 16);
+        const int r = t * 32 + qc;
+        const u32x4 kf = *(const KU_LDS u32x4*)(L + r * RB + (((2 * s + h) ^ kswz(r)) << 4));
 #pragma unroll
         for (int u = 0; u < QT; ++u) sc[u][t] = mfma<DT>(kf, qf[u][s], sc[u][t]);
       }
@@ -227,19 +206,18 @@ attn_mfma_k(AttnArgs a) {
   const float c = a.scale * LOG2E;
   const bool live = qw < S;  // wave-uniform: waves past the sequence only help staging
 
-  loadK(0);
-  loadV(0);
-  storeK(0);
-  storeV(0);
-  loadK(1);
-  storeK(1);
+  dma(K, 0, kbuf(0), false);
+  dma(V, 0, vbuf(0), true);
+  dma(K, 1, kbuf(1), false);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   f32x16 sc[QT][2];
-  s_mfma(ldsk[0], sc);
+  s_mfma(kbuf(0), sc);
 
   for (int kb = 0; kb < nkb; ++kb) {
-    loadK(kb + 2);
-    loadV(kb + 1);
+    // K of block kb+2 and V of block kb+1 into the buffers the previous block freed
+    dma(K, kb + 2, kbuf(kb & 1), false);
+    dma(V, kb + 1, vbuf((kb + 1) & 1), true);
     const int64_t k0 = (int64_t)kb * BK;
     f32x16 sn[QT][2];
     u32x4 pf[QT][4];
@@ -279,7 +257,7 @@ attn_mfma_k(AttnArgs a) {
         }
       }
       // S^T of block kb+1 (its K is already in LDS) interleaved with the exponentials of block kb
-      s_mfma(ldsk[(kb + 1) & 1], sn);
+      s_mfma(kbuf((kb + 1) & 1), sn);
 #pragma unroll
       for (int u = 0; u < QT; ++u) {
         // the row sum adds the rounded probabilities (the ones the P.V product uses), two at a
@@ -304,19 +282,31 @@ attn_mfma_k(AttnArgs a) {
         __builtin_amdgcn_sched_group_barrier(SG_MFMA, QT, 0);
         __builtin_amdgcn_sched_group_barrier(SG_VALU, 96 * QT / (DS * 2), 0);
       }
-      // O^T += V^T . P^T for block kb
+      // O^T += V^T . P^T for block kb. V^T fragments come straight from the row-major V block
+      // with ds_read_b64_tr_b16: in each 16-lane group, input lane 4k'+q points at key row k',
+      // dims 4q..4q+3, and output lane i receives keys 0..3 of dim i. Two reads fetch exactly the
+      // key groups the probability registers hold: 16s + 4h + 0..3 and 16s + 8 + 4h + 0..3.
+      const KU_LDS unsigned char* LV = vbuf(kb & 1);
+      const int g = lane >> 4, c16 = lane & 15;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
         for (int t = 0; t < DTL; ++t) {
-          const u32x4 vf = *reinterpret_cast<const u32x4*>(ldsv[kb & 1] + (t * 32 + qc) * VROW + s * 32 + h * 16);
+          const int d = t * 32 + (g & 1) * 16 + (c16 & 3) * 4;
+          u32x2 half[2];
+#pragma unroll
+          for (int r2 = 0; r2 < 2; ++r2) {
+            const int kr = 16 * s + 8 * r2 + 4 * h + (c16 >> 2);
+            const KU_LDS unsigned char* p = LV + kr * RB + (((d >> 3) ^ vswz(kr)) << 4) + (d & 7) * 2;
+            half[r2] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KU_LDS s16x4*)p));
+          }
+          const u32x4 vf = u32x4{half[0][0], half[0][1], half[1][0], half[1][1]};
 #pragma unroll
           for (int u = 0; u < QT; ++u) o[u][t] = mfma<DT>(vf, pf[u][s], o[u][t]);
         }
     }
-    // stage K of block kb+2 and V of block kb+1 into the buffers freed by the previous block
-    storeK(kb & 1);
-    storeV((kb + 1) & 1);
+    // this thread's DMA for the next blocks has landed; the barrier publishes it
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
 #pragma unroll
     for (int u = 0; u < QT; ++u)
