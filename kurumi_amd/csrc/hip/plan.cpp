@@ -1415,25 +1415,33 @@ std::vector<double> Plan::time_steps(int iters) {
   if (!ctx_) throw Error("plan has no device context");
   ctx_->make_current();
   hipStream_t st = ctx_->stream();
-  size_t n = order_.size();
-  std::vector<hipEvent_t> ev(n + 1);
+  const size_t n = order_.size();
+  iters = std::max(iters, 1);
+  // Events bracket every step of every iteration and are read once at the end: the stream runs
+  // the iterations back to back, as in production, so each step's time is its duration in a
+  // busy pipeline (no idle gap or clock ramp between iterations).
+  std::vector<hipEvent_t> ev((size_t)iters * (n + 1));
   for (auto& e : ev) KU_HIP(hipEventCreate(&e));
-  std::vector<double> acc(n, 0.0);
   for (int it = 0; it < iters; ++it) {
-    KU_HIP(hipEventRecord(ev[0], st));
+    hipEvent_t* e = &ev[(size_t)it * (n + 1)];
+    KU_HIP(hipEventRecord(e[0], st));
     for (size_t i = 0; i < n; ++i) {
       launch_step(steps_[order_[i]]);
-      KU_HIP(hipEventRecord(ev[i + 1], st));
+      KU_HIP(hipEventRecord(e[i + 1], st));
     }
-    KU_HIP(hipEventSynchronize(ev[n]));
+  }
+  KU_HIP(hipEventSynchronize(ev.back()));
+  std::vector<double> acc(n, 0.0);
+  for (int it = 0; it < iters; ++it) {
+    hipEvent_t* e = &ev[(size_t)it * (n + 1)];
     for (size_t i = 0; i < n; ++i) {
       float ms = 0.f;
-      KU_HIP(hipEventElapsedTime(&ms, ev[i], ev[i + 1]));
+      KU_HIP(hipEventElapsedTime(&ms, e[i], e[i + 1]));
       acc[i] += ms;
     }
   }
   for (auto& e : ev) (void)hipEventDestroy(e);
-  for (auto& a : acc) a /= std::max(iters, 1);
+  for (auto& a : acc) a /= iters;
   return acc;
 }
 
