@@ -198,6 +198,22 @@ struct Gen {
   void emit_leaf_load(int ni, const std::string& c_expr);
   void emit_leaf_convert(int ni);
   // argmax/argmin index type along the line (32-bit unless the line is that long)
+  // Non-temporal line-kernel accesses (bit 0 stores, bit 1 loads): a line is read once and its
+  // outputs written once, so neither should displace reused data in L2 / MALL. Stores always;
+  // loads only in regions that also stream a full-size output (a reduce-only region, which
+  // reads far more than it writes, measured slower with non-temporal loads).
+  // KURUMI_HIP_NT overrides.
+  int nt_mode() const {
+    static const int forced = [] {
+      const char* e = std::getenv("KURUMI_HIP_NT");
+      return e ? std::atoi(e) : -1;
+    }();
+    if (forced >= 0) return forced;
+    bool full_out = false;
+    for (auto& op : R.outputs)
+      if (full(op.first)) full_out = true;
+    return full_out ? 3 : 1;
+  }
   // 16-bit leaves are cached two to a 32-bit register
   bool packed_cache(int c) const {
     const RNode& cn = node(c);
@@ -478,8 +494,9 @@ void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
   // r<ni>: the stored bits (what a leaf cache keeps), f<ni>: the compute values
   o << "      " << T << " r" << ni << "[" << V << "];\n";
   if (leaf_vec[n.leaf]) {
-    o << "      { VecT<" << T << ", " << V << "> raw = *(const VecT<" << T << ", " << V << ">*)((const " << T << "*)" << P
-      << " + " << base << " + (" << ix() << ")(" << c_expr << "));\n";
+    const bool ntl = !flat && (nt_mode() & 2);
+    o << "      { VecT<" << T << ", " << V << "> raw = " << (ntl ? "vld_nt(" : "*(") << "(const VecT<" << T << ", " << V
+      << ">*)((const " << T << "*)" << P << " + " << base << " + (" << ix() << ")(" << c_expr << ")));\n";
     o << "        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = raw.v[j]; }\n";
   } else {
     int64_t sa = v.strides[vecaxis];
@@ -833,9 +850,11 @@ std::string Gen::generate(RegionCode* rc) {
         if (d != a) ob << " + (" << ix() << ")c" << d << " * " << rs[d] << "u";
       ob << ")";
       if (V > 1 && rs[a] == 1) {
+        const bool nts = nt_mode() & 1;
         o << "      { VecT<" << T << ", " << V << "> w;\n        #pragma unroll\n        for (int j = 0; j < " << V
-          << "; ++j) w.v[j] = " << st(n.dtype, val(op.first, "j")) << ";\n        *(VecT<" << T << ", " << V << ">*)(("
-          << T << "*)" << Pp << " + " << ob.str() << " + (" << ix() << ")(" << cexpr << ")) = w; }\n";
+          << "; ++j) w.v[j] = " << st(n.dtype, val(op.first, "j")) << ";\n        " << (nts ? "vst_nt(" : "*(")
+          << "(VecT<" << T << ", " << V << ">*)((" << T << "*)" << Pp << " + " << ob.str() << " + (" << ix() << ")("
+          << cexpr << "))" << (nts ? ", w); }\n" : ") = w; }\n");
       } else {
         o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) ((" << T << "*)" << Pp << ")["
           << ob.str() << " + ((" << ix() << ")(" << cexpr << ") + j) * " << rs[a] << "u] = "

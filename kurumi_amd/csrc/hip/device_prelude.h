@@ -16,6 +16,21 @@ typedef unsigned char u8; typedef unsigned short u16; typedef unsigned int u32; 
 typedef signed char i8; typedef short i16; typedef int i32; typedef long long i64;
 template <class T, int N> struct __attribute__((aligned(sizeof(T) * N))) VecT { T v[N]; };
 #define KD __device__ __forceinline__
+// non-temporal 16/8/4-byte vector accesses (streaming data that is touched once)
+typedef u32 ku_u32x4 __attribute__((ext_vector_type(4)));
+typedef u32 ku_u32x2 __attribute__((ext_vector_type(2)));
+template <class V> KD V vld_nt(const V* p) {
+  if constexpr (sizeof(V) == 16) return __builtin_bit_cast(V, __builtin_nontemporal_load((const ku_u32x4*)p));
+  else if constexpr (sizeof(V) == 8) return __builtin_bit_cast(V, __builtin_nontemporal_load((const ku_u32x2*)p));
+  else if constexpr (sizeof(V) == 4) return __builtin_bit_cast(V, __builtin_nontemporal_load((const u32*)p));
+  else return *p;
+}
+template <class V> KD void vst_nt(V* p, const V& v) {
+  if constexpr (sizeof(V) == 16) __builtin_nontemporal_store(__builtin_bit_cast(ku_u32x4, v), (ku_u32x4*)p);
+  else if constexpr (sizeof(V) == 8) __builtin_nontemporal_store(__builtin_bit_cast(ku_u32x2, v), (ku_u32x2*)p);
+  else if constexpr (sizeof(V) == 4) __builtin_nontemporal_store(__builtin_bit_cast(u32, v), (u32*)p);
+  else *p = v;
+}
 KD float bf16_ld(u16 h) { return __uint_as_float(((u32)h) << 16); }
 // v_cvt_pk_bf16_f32: round to nearest even, NaN quieted with its sign and top payload bits kept
 // (the same result as the bit formula u + 0x7fff + lsb >> 16, NaN -> (u >> 16) | 0x40, for all
