@@ -530,7 +530,13 @@ void Gen::emit_full_node(int ni, int phase, const std::string& c_expr) {
   const RNode& n = node(ni);
   bool from_cache = cached.count(ni) && first_phase[ni] < phase;
   if (from_cache) {
-    if (packed_cache(ni)) {
+    if (packed_cache(ni) && R.leaves[n.leaf].dtype == DType::BF16) {
+      // bf16 pairs to f32 without unpacking to 16-bit values: low half << 16, high half masked
+      o << "      float f" << ni << "[" << V << "];\n";
+      o << "      #pragma unroll\n      for (int jj = 0; jj < " << V / 2 << "; ++jj) { f" << ni
+        << "[2 * jj] = __uint_as_float(cache" << ni << "[c][jj] << 16); f" << ni << "[2 * jj + 1] = __uint_as_float(cache"
+        << ni << "[c][jj] & 0xffff0000u); }\n";
+    } else if (packed_cache(ni)) {
       o << "      " << stype(R.leaves[n.leaf].dtype) << " r" << ni << "[" << V << "];\n";
       o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = (u16)(cache" << ni
         << "[c][j >> 1] >> ((j & 1) * 16));\n";
@@ -567,8 +573,28 @@ void Gen::emit_full_node(int ni, int phase, const std::string& c_expr) {
     o << "      }\n";
   } else {
     o << "      " << ctype(n.dtype) << " f" << ni << "[" << V << "];\n";
-    o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) f" << ni << "[j] = " << op_expr(ni, "j")
-      << ";\n";
+    std::string e0 = op_expr(ni, "(2 * jj)"), e1 = op_expr(ni, "(2 * jj + 1)");
+    const std::string pre = "rbf16(";
+    // the whole expression must be one rbf16(...) call: its opening parenthesis closes at the end
+    auto wrapped = [&](const std::string& e) {
+      if (e.compare(0, pre.size(), pre) != 0 || e.back() != ')') return false;
+      int depth = 0;
+      for (size_t i = pre.size() - 1; i < e.size(); ++i) {
+        if (e[i] == '(') ++depth;
+        else if (e[i] == ')' && --depth == 0) return i == e.size() - 1;
+      }
+      return false;
+    };
+    if (n.dtype == DType::BF16 && V % 2 == 0 && wrapped(e0) && wrapped(e1)) {
+      // bf16 results rounded two at a time (one v_cvt_pk_bf16_f32 per pair)
+      e0 = e0.substr(pre.size(), e0.size() - pre.size() - 1);
+      e1 = e1.substr(pre.size(), e1.size() - pre.size() - 1);
+      o << "      #pragma unroll\n      for (int jj = 0; jj < " << V / 2 << "; ++jj) { float a_ = " << e0
+        << "; float b_ = " << e1 << "; rbf16x2(a_, b_); f" << ni << "[2 * jj] = a_; f" << ni << "[2 * jj + 1] = b_; }\n";
+    } else {
+      o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) f" << ni << "[j] = " << op_expr(ni, "j")
+        << ";\n";
+    }
   }
   if (cached.count(ni) && first_phase[ni] == phase) {
     if (packed_cache(ni))
@@ -851,10 +877,18 @@ std::string Gen::generate(RegionCode* rc) {
       ob << ")";
       if (V > 1 && rs[a] == 1) {
         const bool nts = nt_mode() & 1;
-        o << "      { VecT<" << T << ", " << V << "> w;\n        #pragma unroll\n        for (int j = 0; j < " << V
-          << "; ++j) w.v[j] = " << st(n.dtype, val(op.first, "j")) << ";\n        " << (nts ? "vst_nt(" : "*(")
-          << "(VecT<" << T << ", " << V << ">*)((" << T << "*)" << Pp << " + " << ob.str() << " + (" << ix() << ")("
-          << cexpr << "))" << (nts ? ", w); }\n" : ") = w; }\n");
+        if (n.dtype == DType::BF16 && V % 2 == 0 && full(op.first)) {
+          // every bf16 value is carried bf16-exact in f32: its pattern is the upper half
+          o << "      { VecT<u32, " << V / 2 << "> w;\n        #pragma unroll\n        for (int jj = 0; jj < " << V / 2
+            << "; ++jj) w.v[jj] = pack_bf16_exact(" << val(op.first, "2 * jj") << ", " << val(op.first, "2 * jj + 1")
+            << ");\n        " << (nts ? "vst_nt(" : "*(") << "(VecT<u32, " << V / 2 << ">*)((" << T << "*)" << Pp << " + "
+            << ob.str() << " + (" << ix() << ")(" << cexpr << "))" << (nts ? ", w); }\n" : ") = w; }\n");
+        } else {
+          o << "      { VecT<" << T << ", " << V << "> w;\n        #pragma unroll\n        for (int j = 0; j < " << V
+            << "; ++j) w.v[j] = " << st(n.dtype, val(op.first, "j")) << ";\n        " << (nts ? "vst_nt(" : "*(")
+            << "(VecT<" << T << ", " << V << ">*)((" << T << "*)" << Pp << " + " << ob.str() << " + (" << ix() << ")("
+            << cexpr << "))" << (nts ? ", w); }\n" : ") = w; }\n");
+        }
       } else {
         o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) ((" << T << "*)" << Pp << ")["
           << ob.str() << " + ((" << ix() << ")(" << cexpr << ") + j) * " << rs[a] << "u] = "

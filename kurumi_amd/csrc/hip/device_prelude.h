@@ -37,6 +37,16 @@ KD float bf16_ld(u16 h) { return __uint_as_float(((u32)h) << 16); }
 // 2^32 f32 inputs on gfx950)
 KD u16 bf16_st(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
 KD float rbf16(float f) { return bf16_ld(bf16_st(f)); }
+// two roundings with one v_cvt_pk_bf16_f32
+typedef __bf16 ku_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float ku_f32x2 __attribute__((ext_vector_type(2)));
+KD void rbf16x2(float& a, float& b) {
+  const u32 p = __builtin_bit_cast(u32, __builtin_convertvector((ku_f32x2){a, b}, ku_bf16x2));
+  a = __uint_as_float(p << 16);
+  b = __uint_as_float(p & 0xffff0000u);
+}
+// bf16-exact floats (low 16 bits zero) -> two packed bf16 patterns
+KD u32 pack_bf16_exact(float lo, float hi) { return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u); }
 KD float quiet_nan(float f) { return f != f ? __uint_as_float(__float_as_uint(f) | 0x400000u) : f; }
 KD float f16_ld(u16 h) { return (float)__builtin_bit_cast(_Float16, h); }
 KD u16 f16_st(float f) { return __builtin_bit_cast(u16, (_Float16)f); }
