@@ -214,10 +214,22 @@ struct Gen {
       if (full(op.first)) full_out = true;
     return full_out ? 3 : 1;
   }
-  // 16-bit leaves are cached two to a 32-bit register
+  // a vectorised bf16 leaf is loaded and kept as packed 32-bit words
+  bool bf16_words(int c) const {
+    const RNode& cn = node(c);
+    return cn.kind == RK_LEAF && R.leaves[cn.leaf].dtype == DType::BF16 && V % 2 == 0 && leaf_vec[cn.leaf];
+  }
+  // 16-bit leaves are cached two to a 32-bit register. (bf16 intermediates could be too -- every
+  // bf16 value is carried bf16-exact -- but the pack/unpack VALU cost more than the registers
+  // saved in the bf16 softmax, which is VALU-bound; they are cached as f32.)
   bool packed_cache(int c) const {
     const RNode& cn = node(c);
-    return cn.kind == RK_LEAF && dt_width(R.leaves[cn.leaf].dtype) == 2 && V % 2 == 0;
+    if (V % 2 != 0) return false;
+    return cn.kind == RK_LEAF && dt_width(R.leaves[cn.leaf].dtype) == 2;
+  }
+  bool bf16_packed(int c) const {
+    const RNode& cn = node(c);
+    return packed_cache(c) && (cn.kind == RK_LEAF ? R.leaves[cn.leaf].dtype : cn.dtype) == DType::BF16;
   }
   std::string aix() const { return L >= ((uint64_t)1 << 31) ? "i64" : "i32"; }
   std::string aix_none() const { return L >= ((uint64_t)1 << 31) ? "(i64)9223372036854775807ll" : "(i32)2147483647"; }
@@ -448,6 +460,8 @@ void Gen::schedule() {
         cached.insert(c);
         regs += cost_of(c);
       }
+    // a smaller footprint than the budget allows buys more resident waves: ask for them
+    if (!std::getenv("KURUMI_HIP_LINE_WAVES")) min_waves = std::max(min_waves, std::min(8, 512 / (regs + 40)));
   }
   // with caches, later phases need fewer recomputations: rebuild need sets
   if (!cached.empty()) {
@@ -491,6 +505,20 @@ void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
   std::string T = stype(l.dtype), C = ctype(l.dtype);
   std::string P = "p" + std::to_string(slot_param.at(l.slot));
   std::string base = "b" + std::to_string(n.leaf);
+  if (bf16_words(ni)) {
+    // bf16 pairs stay packed in 32-bit words (the form the cache keeps); each value is its word's
+    // low half shifted up or its high half masked
+    const bool ntl = !flat && (nt_mode() & 2);
+    o << "      u32 rw" << ni << "[" << V / 2 << "];\n";
+    o << "      { VecT<u32, " << V / 2 << "> raw = " << (ntl ? "vld_nt(" : "*(") << "(const VecT<u32, " << V / 2
+      << ">*)((const " << T << "*)" << P << " + " << base << " + (" << ix() << ")(" << c_expr << ")));\n";
+    o << "        #pragma unroll\n        for (int jj = 0; jj < " << V / 2 << "; ++jj) rw" << ni << "[jj] = raw.v[jj]; }\n";
+    o << "      float f" << ni << "[" << V << "];\n";
+    o << "      #pragma unroll\n      for (int jj = 0; jj < " << V / 2 << "; ++jj) { f" << ni
+      << "[2 * jj] = __uint_as_float(rw" << ni << "[jj] << 16); f" << ni << "[2 * jj + 1] = __uint_as_float(rw" << ni
+      << "[jj] & 0xffff0000u); }\n";
+    return;
+  }
   // r<ni>: the stored bits (what a leaf cache keeps), f<ni>: the compute values
   o << "      " << T << " r" << ni << "[" << V << "];\n";
   if (leaf_vec[n.leaf]) {
@@ -530,7 +558,7 @@ void Gen::emit_full_node(int ni, int phase, const std::string& c_expr) {
   const RNode& n = node(ni);
   bool from_cache = cached.count(ni) && first_phase[ni] < phase;
   if (from_cache) {
-    if (packed_cache(ni) && R.leaves[n.leaf].dtype == DType::BF16) {
+    if (bf16_packed(ni)) {
       // bf16 pairs to f32 without unpacking to 16-bit values: low half << 16, high half masked
       o << "      float f" << ni << "[" << V << "];\n";
       o << "      #pragma unroll\n      for (int jj = 0; jj < " << V / 2 << "; ++jj) { f" << ni
@@ -597,7 +625,13 @@ void Gen::emit_full_node(int ni, int phase, const std::string& c_expr) {
     }
   }
   if (cached.count(ni) && first_phase[ni] == phase) {
-    if (packed_cache(ni))
+    if (bf16_words(ni))
+      o << "      #pragma unroll\n      for (int jj = 0; jj < " << V / 2 << "; ++jj) cache" << ni << "[c][jj] = rw" << ni
+        << "[jj];\n";
+    else if (bf16_packed(ni) && n.kind != RK_LEAF)
+      o << "      #pragma unroll\n      for (int jj = 0; jj < " << V / 2 << "; ++jj) cache" << ni
+        << "[c][jj] = pack_bf16_exact(f" << ni << "[2 * jj], f" << ni << "[2 * jj + 1]);\n";
+    else if (packed_cache(ni))
       o << "      #pragma unroll\n      for (int j = 0; j < " << V / 2 << "; ++j) cache" << ni << "[c][j] = (u32)r" << ni
         << "[2 * j] | ((u32)r" << ni << "[2 * j + 1] << 16);\n";
     else
