@@ -380,6 +380,9 @@ void Gen::plan_layout() {
   if (const char* e = std::getenv("KURUMI_HIP_LINE_CHUNKS")) target = std::max(1, std::atoi(e));
   uint64_t t = 1;
   while (t < 1024 && t * (uint64_t)target < chunks) t *= 2;
+  // few lines: spread each over more threads (down to 2 chunks per thread) until the launch has
+  // about 16 waves per CU to hide memory latency with
+  while (t < 1024 && lines * t < ((uint64_t)1 << 18) && chunks >= 4 * t) t *= 2;
   TPL = (int)t;
   NC = (int)((chunks + TPL - 1) / TPL);
   WG = std::max(TPL, 256);

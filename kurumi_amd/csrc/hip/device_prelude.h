@@ -59,48 +59,31 @@ KD float f32_odd(double x) {
 }
 KD float rbf16_d(double x) { return rbf16(f32_odd(x)); }
 KD float rf16_d(double x) { return rf16(f32_odd(x)); }
+// decodes: v_cvt_f32_fp8 / v_cvt_f32_bf8, NaN codes produced here (e4m3 S.1111.111 -> quiet NaN
+// with the sign; e5m2 NaN keeps sign and payload, quiet bit set, like the half crate's f16 path)
 KD float f8e4m3_ld(u8 b) {
-  u32 e = (b >> 3) & 15u, m = b & 7u;
-  float v;
-  if (e == 15u && m == 7u) v = __uint_as_float(0x7fc00000u);
-  else if (e == 0u) v = (float)m * 0.001953125f;
-  else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
-  return (b & 0x80u) ? -v : v;
+  const float v = __builtin_amdgcn_cvt_f32_fp8((u32)b, 0);
+  const float nan = __uint_as_float(((u32)(b & 0x80u) << 24) | 0x7fc00000u);
+  return (b & 0x7fu) == 0x7fu ? nan : v;
 }
+// OCP e4m3: nearest even, saturating to +-448, NaN -> S.1111.111 (v_cvt_pk_fp8_f32 on the input
+// clamped to +-448 gives the bit-level rounding's codes for all 2^32 f32 inputs on gfx950)
 KD u8 f8e4m3_st(float x) {
-  u32 u = __float_as_uint(x);
-  u32 s = (u >> 24) & 0x80u;
-  if (x != x) return (u8)(s | 0x7fu);
-  float a = fabsf(x);
-  if (a > 448.f) return (u8)(s | 0x7eu);
-  if (a < 0.015625f) return (u8)(s | (u32)rintf(a * 512.f));
-  int E = (int)((u >> 23) & 0xffu) - 127;
-  float q = __uint_as_float((u32)(E - 3 + 127) << 23);
-  u32 n = (u32)rintf(a / q);
-  u32 r = ((u32)(E + 7) << 3) + (n - 8u);
-  if (r > 0x7eu) r = 0x7eu;
-  return (u8)(s | r);
+  const u32 c = (u32)__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(x, -448.f, 448.f), 0.f, 0, false) & 0xffu;
+  const u32 nan = ((__float_as_uint(x) >> 24) & 0x80u) | 0x7fu;
+  return (u8)(x != x ? nan : c);
 }
 KD float rf8e4m3(float x) { return f8e4m3_ld(f8e4m3_st(x)); }
 KD float f8e5m2_ld(u8 b) {
-  u32 e = (b >> 2) & 31u, m = b & 3u;
-  float v;
-  if (e == 31u) v = m ? __uint_as_float(0x7fc00000u) : INFINITY;
-  else if (e == 0u) v = (float)m * 1.52587890625e-05f;
-  else v = __uint_as_float(((e + 112u) << 23) | (m << 21));
-  return (b & 0x80u) ? -v : v;
+  const float v = __builtin_amdgcn_cvt_f32_bf8((u32)b, 0);
+  const float nan = __uint_as_float(((u32)(b & 0x80u) << 24) | 0x7fc00000u | ((u32)(b & 3u) << 21));
+  return ((b & 0x7cu) == 0x7cu && (b & 3u)) ? nan : v;
 }
+// OCP e5m2: nearest even, overflow to inf, NaN -> S.11111.10 (v_cvt_pk_bf8_f32)
 KD u8 f8e5m2_st(float x) {
-  u32 u = __float_as_uint(x);
-  u32 s = (u >> 24) & 0x80u;
-  if (x != x) return (u8)(s | 0x7eu);
-  float a = fabsf(x);
-  if (a >= 61440.f) return (u8)(s | 0x7cu);
-  if (a < 6.103515625e-05f) return (u8)(s | (u32)rintf(a * 65536.f));
-  int E = (int)((u >> 23) & 0xffu) - 127;
-  float q = __uint_as_float((u32)(E - 2 + 127) << 23);
-  u32 n = (u32)rintf(a / q);
-  return (u8)(s | (((u32)(E + 15) << 2) + (n - 4u)));
+  const u32 c = (u32)__builtin_amdgcn_cvt_pk_bf8_f32(x, 0.f, 0, false) & 0xffu;
+  const u32 nan = ((__float_as_uint(x) >> 24) & 0x80u) | 0x7eu;
+  return (u8)(x != x ? nan : c);
 }
 KD float rf8e5m2(float x) { return f8e5m2_ld(f8e5m2_st(x)); }
 template <class I> KD I sat_int(double x);

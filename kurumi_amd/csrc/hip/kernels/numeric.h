@@ -19,47 +19,28 @@ __device__ __forceinline__ float d_bf16_ld(uint16_t h) { return __uint_as_float(
 __device__ __forceinline__ uint16_t d_bf16_st(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 __device__ __forceinline__ float d_f16_ld(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t d_f16_st(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// v_cvt_f32_fp8, with the NaN code S.1111.111 decoded to a quiet NaN carrying the sign
 __device__ __forceinline__ float d_e4m3_ld(uint8_t b) {
-  uint32_t e = (b >> 3) & 15u, m = b & 7u;
-  float v;
-  if (e == 15u && m == 7u) v = __uint_as_float(0x7fc00000u);
-  else if (e == 0u) v = (float)m * 0.001953125f;
-  else v = __uint_as_float(((e + 120u) << 23) | (m << 20));
-  return (b & 0x80u) ? -v : v;
+  if ((b & 0x7fu) == 0x7fu) return __uint_as_float(((uint32_t)(b & 0x80u) << 24) | 0x7fc00000u);
+  return __builtin_amdgcn_cvt_f32_fp8((uint32_t)b, 0);
 }
+// OCP e4m3 (E4M3FN), round to nearest even, saturating to +-448, NaN -> S.1111.111:
+// v_cvt_pk_fp8_f32 on the input clamped to +-448 (the same codes as the bit-level rounding for all
+// 2^32 f32 inputs on gfx950)
 __device__ __forceinline__ uint8_t d_e4m3_st(float x) {
-  uint32_t u = __float_as_uint(x);
-  uint32_t s = (u >> 24) & 0x80u;
-  if (x != x) return (uint8_t)(s | 0x7fu);
-  float a = fabsf(x);
-  if (a > 448.f) return (uint8_t)(s | 0x7eu);
-  if (a < 0.015625f) return (uint8_t)(s | (uint32_t)rintf(a * 512.f));
-  int E = (int)((u >> 23) & 0xffu) - 127;
-  float q = __uint_as_float((uint32_t)(E - 3 + 127) << 23);
-  uint32_t n = (uint32_t)rintf(a / q);
-  uint32_t r = ((uint32_t)(E + 7) << 3) + (n - 8u);
-  if (r > 0x7eu) r = 0x7eu;
-  return (uint8_t)(s | r);
+  if (x != x) return (uint8_t)(((__float_as_uint(x) >> 24) & 0x80u) | 0x7fu);
+  return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(__builtin_amdgcn_fmed3f(x, -448.f, 448.f), 0.f, 0, false) & 0xffu);
 }
+// v_cvt_f32_bf8, NaN codes keeping sign and payload (quiet bit set)
 __device__ __forceinline__ float d_e5m2_ld(uint8_t b) {
-  uint32_t e = (b >> 2) & 31u, m = b & 3u;
-  float v;
-  if (e == 31u) v = m ? __uint_as_float(0x7fc00000u) : INFINITY;
-  else if (e == 0u) v = (float)m * 1.52587890625e-05f;
-  else v = __uint_as_float(((e + 112u) << 23) | (m << 21));
-  return (b & 0x80u) ? -v : v;
+  if ((b & 0x7cu) == 0x7cu && (b & 3u))
+    return __uint_as_float(((uint32_t)(b & 0x80u) << 24) | 0x7fc00000u | ((uint32_t)(b & 3u) << 21));
+  return __builtin_amdgcn_cvt_f32_bf8((uint32_t)b, 0);
 }
+// OCP e5m2, round to nearest even, overflow to inf, NaN -> S.11111.10: v_cvt_pk_bf8_f32
 __device__ __forceinline__ uint8_t d_e5m2_st(float x) {
-  uint32_t u = __float_as_uint(x);
-  uint32_t s = (u >> 24) & 0x80u;
-  if (x != x) return (uint8_t)(s | 0x7eu);
-  float a = fabsf(x);
-  if (a >= 61440.f) return (uint8_t)(s | 0x7cu);
-  if (a < 6.103515625e-05f) return (uint8_t)(s | (uint32_t)rintf(a * 65536.f));
-  int E = (int)((u >> 23) & 0xffu) - 127;
-  float q = __uint_as_float((uint32_t)(E - 2 + 127) << 23);
-  uint32_t n = (uint32_t)rintf(a / q);
-  return (uint8_t)(s | (((uint32_t)(E + 15) << 2) + (n - 4u)));
+  if (x != x) return (uint8_t)(((__float_as_uint(x) >> 24) & 0x80u) | 0x7eu);
+  return (uint8_t)(__builtin_amdgcn_cvt_pk_bf8_f32(x, 0.f, 0, false) & 0xffu);
 }
 
 // storage element -> accumulation type

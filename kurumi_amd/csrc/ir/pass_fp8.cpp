@@ -5,7 +5,7 @@
 // to f8 (interp/contract.rs:57-64). This pass is the e4m3 policy of the quantized-linear
 // workload: a `DotGeneral(x, w; lc=[1], rc=[1])` with a 2-D floating x and weight w becomes
 //
-//   sx = reduce_max(reduce_max(|x|, 1), 0) / 448            (per-tensor, in-graph)
+//   sx = reduce_max(reduce_max(|x|, 1), 0) * (1/448)        (per-tensor, in-graph)
 //   xq = cast_e4m3(x * (1/sx))
 //   sw[n] = max_k |w[n,k]| / 448, wq = cast_e4m3(w / sw[n])  (per row; host-side when w is a Const)
 //   y  = cast_out( dot(cast_f32(xq), cast_f32(wq)) * sx * sw[n] )
@@ -18,6 +18,13 @@
 #include <unordered_map>
 
 #include "graph.h"
+
+namespace {
+// a / 448 in the graph's terms: div(a, b) is mul(a, recip(b)), and recip of the constant 448 is
+// the correctly rounded f32 1/448, so multiplying by this constant is the same value bit for bit
+// (and needs no device work to divide a constant)
+constexpr float kInv448 = 1.0f / 448.0f;
+}  // namespace
 
 namespace ku {
 
@@ -116,8 +123,7 @@ NodeId amp_fp8(Graph& g, NodeId root) {
         NodeId wf = g.dtype(w) == DType::F32 ? w : g.cast(w, DType::F32);
         NodeId wa = g.max(wf, g.neg(wf));
         NodeId wm = g.reduce_max(wa, 1);
-        NodeId c448 = g.scalar(wm, 448.0f);
-        sw_node = g.div(wm, c448);
+        sw_node = g.mul(wm, g.scalar(wm, kInv448));
         NodeId inv = g.recip(sw_node);
         NodeId invb = g.broadcast_back(inv, {N, K}, 1);
         wq_node = g.cast(g.mul(wf, invb), DType::F8E4M3);
@@ -127,11 +133,13 @@ NodeId amp_fp8(Graph& g, NodeId root) {
       NodeId xa = g.max(xf, g.neg(xf));
       NodeId rm = g.reduce_max(xa, 1);
       NodeId am = g.reduce_max(rm, 0);
-      NodeId c448 = g.scalar(am, 448.0f);
-      NodeId sx = g.div(am, c448);
+      NodeId sx = g.mul(am, g.scalar(am, kInv448));
       NodeId inv = g.recip(sx);
       NodeId invb = g.expand(g.reshape(inv, {1, 1}), {M, K});
-      NodeId xq = g.cast(g.mul(xf, invb), DType::F8E4M3);
+      // The quantisation gets its own cast of x: the absmax pass and the quantise pass then each
+      // read x in its own (16-bit) storage, instead of sharing an f32 copy written to HBM.
+      NodeId xf2 = g.dtype(x) == DType::F32 ? x : g.cast(x, DType::F32);
+      NodeId xq = g.cast(g.mul(xf2, invb), DType::F8E4M3);
       NodeId d = g.dot_general(g.cast(xq, DType::F32), g.cast(wq_node, DType::F32), {1}, {1}, {}, {});
       NodeId y1 = g.mul(d, g.expand(g.reshape(sx, {1, 1}), {M, N}));
       NodeId y2 = g.mul(y1, g.expand(g.reshape(sw_node, {1, N}), {M, N}));

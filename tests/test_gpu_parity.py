@@ -382,7 +382,7 @@ def test_missing_feed_is_an_error(hip):
         hip.eval_with(g, y, {})
 
 
-@pytest.mark.parametrize("to", [DType.BF16, DType.F16])
+@pytest.mark.parametrize("to", [DType.BF16, DType.F16, DType.F8E4M3, DType.F8E5M2])
 def test_f32_to_half_casts_bit_exact_across_the_bit_space(hip, to):
     # every 257th f32 bit pattern (all exponents, signs, NaN payloads, denormals) plus the
     # rounding ties around each half-precision step
@@ -398,10 +398,11 @@ def test_f32_to_half_casts_bit_exact_across_the_bit_space(hip, to):
     np.testing.assert_array_equal(got, want)
 
 
-@pytest.mark.parametrize("frm", [DType.BF16, DType.F16])
+@pytest.mark.parametrize("frm", [DType.BF16, DType.F16, DType.F8E4M3, DType.F8E5M2])
 @pytest.mark.parametrize("to", [DType.F32, DType.F64, DType.I32])
 def test_half_casts_bit_exact_for_every_pattern(hip, frm, to):
-    bits = np.arange(0, 1 << 16, dtype=np.uint32).astype(np.uint16)
+    width = 16 if frm in (DType.BF16, DType.F16) else 8
+    bits = np.arange(0, 1 << width, dtype=np.uint32).astype(np.uint16 if width == 16 else np.uint8)
     g = Graph()
     x = g.input([bits.size], frm)
     c = g.cast(x, to)
