@@ -51,16 +51,24 @@ def scaled_randn(std):
 
 
 def time_plan(plan, steps: int, warmup: int, use_graph: bool = False):
+    """Warm up, then the timed region: `steps` back-to-back launches of the plan on its stream,
+    bracketed by hipEvents on that stream (ku_hip_plan_time) and by a host clock around the call,
+    which ends with the stream drained. Returns (wall ms per step, GPU ms of each plan step,
+    step labels): the GPU time per launch comes from the timed region's events; a following
+    run with events between the steps only splits it among the steps of a multi-kernel plan."""
     for _ in range(warmup):
         plan.launch(use_graph)
     plan.sync()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        plan.launch(use_graph)
-    plan.sync()
+    gpu_ms = plan.time(steps, use_graph)
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    per_step = plan.time_steps(max(steps, 5))
-    return wall_ms, per_step, plan.steps()
+    labels = plan.steps()
+    if len(labels) == 1:
+        return wall_ms, [gpu_ms], labels
+    shares = plan.time_steps(max(steps, 5))
+    tot = sum(shares)
+    per_step = [s / tot * gpu_ms for s in shares] if tot > 0 else shares
+    return wall_ms, per_step, labels
 
 
 def measured_traffic(kernel: str):

@@ -1417,9 +1417,28 @@ std::vector<double> Plan::time_steps(int iters) {
   hipStream_t st = ctx_->stream();
   const size_t n = order_.size();
   iters = std::max(iters, 1);
-  // Events bracket every step of every iteration and are read once at the end: the stream runs
-  // the iterations back to back, as in production, so each step's time is its duration in a
-  // busy pipeline (no idle gap or clock ramp between iterations).
+  // Two back-to-back runs of `iters` iterations on the plan's stream (events read once at the
+  // end, so the stream never idles): one bracketed by a single pair of events gives the time per
+  // iteration; one with events between the steps gives each step's share of it. An event between
+  // two kernels keeps the next from starting until the previous has drained, so the per-step
+  // events alone would charge every step that drain.
+  hipEvent_t t0, t1;
+  KU_HIP(hipEventCreate(&t0));
+  KU_HIP(hipEventCreate(&t1));
+  KU_HIP(hipEventRecord(t0, st));
+  for (int it = 0; it < iters; ++it)
+    for (size_t i = 0; i < n; ++i) launch_step(steps_[order_[i]]);
+  KU_HIP(hipEventRecord(t1, st));
+  KU_HIP(hipEventSynchronize(t1));
+  float whole = 0.f;
+  KU_HIP(hipEventElapsedTime(&whole, t0, t1));
+  (void)hipEventDestroy(t0);
+  (void)hipEventDestroy(t1);
+  std::vector<double> acc(n, 0.0);
+  if (n == 1) {
+    acc[0] = whole / iters;
+    return acc;
+  }
   std::vector<hipEvent_t> ev((size_t)iters * (n + 1));
   for (auto& e : ev) KU_HIP(hipEventCreate(&e));
   for (int it = 0; it < iters; ++it) {
@@ -1431,17 +1450,18 @@ std::vector<double> Plan::time_steps(int iters) {
     }
   }
   KU_HIP(hipEventSynchronize(ev.back()));
-  std::vector<double> acc(n, 0.0);
+  double sum = 0.0;
   for (int it = 0; it < iters; ++it) {
     hipEvent_t* e = &ev[(size_t)it * (n + 1)];
     for (size_t i = 0; i < n; ++i) {
       float ms = 0.f;
       KU_HIP(hipEventElapsedTime(&ms, e[i], e[i + 1]));
       acc[i] += ms;
+      sum += ms;
     }
   }
   for (auto& e : ev) (void)hipEventDestroy(e);
-  for (auto& a : acc) a /= iters;
+  for (auto& a : acc) a = sum > 0 ? a / sum * (whole / iters) : a / iters;
   return acc;
 }
 
