@@ -736,6 +736,13 @@ void Gen::emit_red_finish(int ni, int phase) {
     return "acc" + r + " = (" + ov + " > acc" + r + ") ? " + ov + " : acc" + r + ";";
   };
   int wl = std::min(TPL, 64);
+  const bool fsum = n.kind == (int)OpKind::Sum && (fvalued(n.dtype) || in == DType::F32);
+  const bool fmax = n.kind == (int)OpKind::ReduceMax && (fvalued(n.dtype) || in == DType::F32);
+  static const bool no_dpp = std::getenv("KURUMI_HIP_NO_DPP") != nullptr;
+  if (!arg && wl == 64 && (fsum || fmax) && !no_dpp) {
+    o << "  acc" << r << " = " << (fsum ? "wave_sum(" : "wave_max(") << "acc" << r << ");\n";
+    wl = 1;  // folded; the loop below does nothing
+  }
   for (int m = wl / 2; m >= 1; m /= 2) {
     if (arg)
       o << "  { " << ctype(in) << " ov = shx(bv" << r << ", " << m << "); " << aix() << " oi = shx(bi" << r << ", " << m

@@ -107,6 +107,31 @@ KD u64 threefry2x32(u64 key, u64 ctr) {
 }
 KD float uniform_f32(u64 bits) { return (float)((u32)bits >> 8) / 16777216.f; }
 KD float shx(float v, int m) { return __shfl_xor(v, m, 64); }
+// wave64 reductions on DPP row shifts and row broadcasts (lane 63 ends with the total, which
+// v_readlane hands to every lane): VALU latency instead of an LDS permute per step
+template <int CTRL, int ROW_MASK> KD float dppf(float old, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old), __builtin_bit_cast(int, v),
+                                                                CTRL, ROW_MASK, 0xf, false));
+}
+KD float wave_sum(float v) {
+  v += dppf<0x111, 0xf>(0.f, v);  // row_shr:1
+  v += dppf<0x112, 0xf>(0.f, v);  // row_shr:2
+  v += dppf<0x114, 0xf>(0.f, v);  // row_shr:4
+  v += dppf<0x118, 0xf>(0.f, v);  // row_shr:8 -> lane 15 of each row holds the row
+  v += dppf<0x142, 0xa>(0.f, v);  // row_bcast:15 into rows 1, 3
+  v += dppf<0x143, 0xc>(0.f, v);  // row_bcast:31 into rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+KD float wave_max(float v) {
+  const float ni = -INFINITY;
+  v = fmaxf(v, dppf<0x111, 0xf>(ni, v));
+  v = fmaxf(v, dppf<0x112, 0xf>(ni, v));
+  v = fmaxf(v, dppf<0x114, 0xf>(ni, v));
+  v = fmaxf(v, dppf<0x118, 0xf>(ni, v));
+  v = fmaxf(v, dppf<0x142, 0xa>(ni, v));
+  v = fmaxf(v, dppf<0x143, 0xc>(ni, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
 KD double shx(double v, int m) { return __shfl_xor(v, m, 64); }
 KD i32 shx(i32 v, int m) { return __shfl_xor(v, m, 64); }
 KD u32 shx(u32 v, int m) { return __shfl_xor((i32)v, m, 64); }
