@@ -43,6 +43,7 @@ typedef struct KuFeeds KuFeeds;
 typedef struct KuBackend KuBackend;
 typedef struct KuPlan KuPlan;
 typedef struct KuHipPlan KuHipPlan;
+typedef struct KuRunnable KuRunnable;
 typedef uint32_t KuNode;
 
 const char *ku_last_error(void); /* kurumi.h:51 */
@@ -143,6 +144,39 @@ size_t ku_dump(const KuGraph *g, KuNode root, uint8_t *out, size_t cap);
 size_t ku_node_rank(const KuGraph *g, KuNode node);
 void ku_node_shape(const KuGraph *g, KuNode node, size_t *out);
 uint32_t ku_node_dtype(const KuGraph *g, KuNode node);
+
+/* runnable-graph serialization, KGPH v2 blobs: kurumi.h:407-453. Inputs bind by (node, role,
+ * name): role 0 = weight (bound by name), 1 = runtime feed; in_names are NUL-terminated UTF-8.
+ * Size-then-write: cap=0 with out=NULL returns the length (0 and ku_last_error on failure). */
+size_t ku_graph_serialize(const KuGraph *g, const KuNode *outputs, size_t n_out, const KuNode *in_nodes,
+                          const uint8_t *in_roles, const char *const *in_names, size_t n_in, uint8_t *out, size_t cap);
+size_t ku_graph_serialize_reachable(const KuGraph *g, const KuNode *outputs, size_t n_out, const KuNode *in_nodes,
+                                    const uint8_t *in_roles, const char *const *in_names, size_t n_in, uint8_t *out,
+                                    size_t cap);
+size_t ku_graph_serialize_multi(const KuGraph *g, size_t n_entries, const char *const *names,
+                                const uint32_t *out_counts, const KuNode *outputs, const uint32_t *in_counts,
+                                const KuNode *in_nodes, const uint8_t *in_roles, const char *const *in_names,
+                                uint8_t *out, size_t cap);
+/* NULL (see ku_last_error) on a malformed or entry-less blob; every node is replayed through
+ * the checked builders. Ops outside this IR (QuantMatmul, linalg, complex, gather/scatter,
+ * argsort) are rejected with their name. */
+KuRunnable *ku_graph_deserialize(const uint8_t *bytes, size_t len);
+KuGraph *ku_runnable_take_graph(KuRunnable *h);
+size_t ku_runnable_output_count(const KuRunnable *h);
+KuNode ku_runnable_output(const KuRunnable *h, size_t i);
+size_t ku_runnable_input_count(const KuRunnable *h);
+KuNode ku_runnable_input_node(const KuRunnable *h, size_t i);
+uint32_t ku_runnable_input_role(const KuRunnable *h, size_t i);
+size_t ku_runnable_input_name(const KuRunnable *h, size_t i, uint8_t *out, size_t cap);
+size_t ku_runnable_entry_count(const KuRunnable *h);
+size_t ku_runnable_entry_name(const KuRunnable *h, size_t i, uint8_t *out, size_t cap);
+size_t ku_runnable_entry_output_count(const KuRunnable *h, size_t i);
+KuNode ku_runnable_entry_output(const KuRunnable *h, size_t i, size_t j);
+size_t ku_runnable_entry_input_count(const KuRunnable *h, size_t i);
+KuNode ku_runnable_entry_input_node(const KuRunnable *h, size_t i, size_t j);
+uint32_t ku_runnable_entry_input_role(const KuRunnable *h, size_t i, size_t j);
+size_t ku_runnable_entry_input_name(const KuRunnable *h, size_t i, size_t j, uint8_t *out, size_t cap);
+void ku_runnable_free(KuRunnable *h);
 
 /* plan-replay: kurumi.h:456-458. Here the plan is a device plan on the process's default
  * KU_HIP backend (device 0), replayed as one hipGraph launch per run. */

@@ -147,6 +147,30 @@ def _declare(L: C.CDLL) -> None:
         "ku_hip_plan_free": ([P], None),
         "ku_hip_codegen": ([P, C.POINTER(C.c_uint32), sz, u32, C.c_char_p, sz], sz),
         "ku_hip_profile": ([P, C.POINTER(C.c_uint64), sz], C.c_uint64),
+        "ku_graph_serialize": ([P, C.POINTER(u32), sz, C.POINTER(u32), C.POINTER(C.c_uint8),
+                                C.POINTER(C.c_char_p), sz, C.c_char_p, sz], sz),
+        "ku_graph_serialize_reachable": ([P, C.POINTER(u32), sz, C.POINTER(u32), C.POINTER(C.c_uint8),
+                                          C.POINTER(C.c_char_p), sz, C.c_char_p, sz], sz),
+        "ku_graph_serialize_multi": ([P, sz, C.POINTER(C.c_char_p), C.POINTER(u32), C.POINTER(u32), C.POINTER(u32),
+                                      C.POINTER(u32), C.POINTER(C.c_uint8), C.POINTER(C.c_char_p), C.c_char_p, sz],
+                                     sz),
+        "ku_graph_deserialize": ([C.c_char_p, sz], P),
+        "ku_runnable_take_graph": ([P], P),
+        "ku_runnable_output_count": ([P], sz),
+        "ku_runnable_output": ([P, sz], u32),
+        "ku_runnable_input_count": ([P], sz),
+        "ku_runnable_input_node": ([P, sz], u32),
+        "ku_runnable_input_role": ([P, sz], u32),
+        "ku_runnable_input_name": ([P, sz, C.c_char_p, sz], sz),
+        "ku_runnable_entry_count": ([P], sz),
+        "ku_runnable_entry_name": ([P, sz, C.c_char_p, sz], sz),
+        "ku_runnable_entry_output_count": ([P, sz], sz),
+        "ku_runnable_entry_output": ([P, sz, sz], u32),
+        "ku_runnable_entry_input_count": ([P, sz], sz),
+        "ku_runnable_entry_input_node": ([P, sz, sz], u32),
+        "ku_runnable_entry_input_role": ([P, sz, sz], u32),
+        "ku_runnable_entry_input_name": ([P, sz, sz, C.c_char_p, sz], sz),
+        "ku_runnable_free": ([P], None),
     }
     for name in ["ku_add", "ku_sub", "ku_mul", "ku_div", "ku_max", "ku_idiv", "ku_and", "ku_or", "ku_xor", "ku_shl",
                  "ku_shr", "ku_lt", "ku_eq", "ku_matmul"]:
@@ -247,8 +271,8 @@ class Feeds:
 class Graph:
     """Append-only graph builder (kurumi_core/src/graph.rs); methods return node ids."""
 
-    def __init__(self):
-        self.h = lib().ku_graph_new()
+    def __init__(self, _handle=None):
+        self.h = _handle if _handle else lib().ku_graph_new()
 
     def __del__(self):
         if getattr(self, "h", None) and _lib is not None:
@@ -423,6 +447,136 @@ for _n, _c in [("sum", "ku_sum"), ("prod", "ku_prod"), ("mean", "ku_mean"), ("re
                ("argmax", "ku_argmax"), ("argmin", "ku_argmin"), ("softmax", "ku_softmax"),
                ("squeeze", "ku_squeeze"), ("unsqueeze", "ku_unsqueeze")]:
     _add_simple(_n, _c, 3)
+
+
+# ---- KGPH v2 graph blobs (kurumi_core/src/graph/serialize.rs; C ABI kurumi.h:407-453) ----
+
+class InputRole(enum.IntEnum):
+    """serialize.rs:28-33: a weight is bound by name from a weight table, a runtime input is fed."""
+    Weight = 0
+    Runtime = 1
+
+
+class InputBinding(tuple):
+    """(node, role, name) of one entry input (serialize.rs:35-41)."""
+    __slots__ = ()
+
+    def __new__(cls, node: int, role: InputRole, name: str):
+        return super().__new__(cls, (int(node), InputRole(role), str(name)))
+
+    node = property(lambda self: self[0])
+    role = property(lambda self: self[1])
+    name = property(lambda self: self[2])
+
+
+class Entry:
+    """One named entry point of a blob: its output node ids and input bindings."""
+
+    def __init__(self, name: str, outputs: Sequence[int], inputs: Sequence[InputBinding]):
+        self.name, self.outputs, self.inputs = name, list(outputs), list(inputs)
+
+    def __repr__(self):
+        return f"Entry({self.name!r}, outputs={self.outputs}, inputs={self.inputs})"
+
+
+class Runnable:
+    """A decoded blob: the rebuilt graph (ids preserved) and every entry (``MultiRunnable``).
+    ``outputs``/``inputs`` are entry 0's, as in ``deserialize_graph``'s ``Runnable``."""
+
+    def __init__(self, graph: Graph, entries: list[Entry]):
+        self.graph, self.entries = graph, entries
+
+    @property
+    def outputs(self) -> list[int]:
+        return self.entries[0].outputs
+
+    @property
+    def inputs(self) -> list[InputBinding]:
+        return self.entries[0].inputs
+
+
+def _bind_arrays(inputs: Sequence[InputBinding]):
+    n = len(inputs)
+    nodes = (C.c_uint32 * max(n, 1))(*[b[0] for b in inputs])
+    roles = (C.c_uint8 * max(n, 1))(*[int(b[1]) for b in inputs])
+    names = (C.c_char_p * max(n, 1))(*[str(b[2]).encode() for b in inputs])
+    return nodes, roles, names
+
+
+def _size_then_write(call) -> bytes:
+    n = call(None, 0)
+    if n == 0:  # a blob holds at least its magic, version and two counts: 0 is the error answer
+        raise KuError(last_error())
+    buf = C.create_string_buffer(max(n, 1))
+    m = call(buf, n)
+    if m != n:
+        raise KuError(f"serialize: length changed {n} -> {m}")
+    return buf.raw[:n]
+
+
+def _serialize(cname: str, g: Graph, outputs: Sequence[int], inputs: Sequence[InputBinding]) -> bytes:
+    outs = (C.c_uint32 * max(len(outputs), 1))(*outputs)
+    nodes, roles, names = _bind_arrays(inputs)
+    f = getattr(lib(), cname)
+    return _size_then_write(lambda out, cap: f(g.h, outs, len(outputs), nodes, roles, names, len(inputs), out, cap))
+
+
+def serialize_graph(g: Graph, outputs: Sequence[int], inputs: Sequence[InputBinding] = ()) -> bytes:
+    """The whole arena in id order, one entry named "" (encode.rs:26-34)."""
+    return _serialize("ku_graph_serialize", g, outputs, inputs)
+
+
+def serialize_reachable(g: Graph, outputs: Sequence[int], inputs: Sequence[InputBinding] = ()) -> bytes:
+    """Only the outputs' cone, dense-remapped; unreachable bindings dropped (encode.rs:42-44)."""
+    return _serialize("ku_graph_serialize_reachable", g, outputs, inputs)
+
+
+def serialize_multi(g: Graph, entries: Sequence[tuple[str, Sequence[int], Sequence[InputBinding]]]) -> bytes:
+    """N named entries over one arena, pruned to the union of their cones (encode.rs:50-53)."""
+    ne = len(entries)
+    names = (C.c_char_p * max(ne, 1))(*[e[0].encode() for e in entries])
+    oc = (C.c_uint32 * max(ne, 1))(*[len(e[1]) for e in entries])
+    ic = (C.c_uint32 * max(ne, 1))(*[len(e[2]) for e in entries])
+    flat_out = [o for e in entries for o in e[1]]
+    outs = (C.c_uint32 * max(len(flat_out), 1))(*flat_out)
+    nodes, roles, in_names = _bind_arrays([b for e in entries for b in e[2]])
+    f = lib().ku_graph_serialize_multi
+    return _size_then_write(lambda out, cap: f(g.h, ne, names, oc, outs, ic, nodes, roles, in_names, out, cap))
+
+
+def _name(call) -> str:
+    n = call(None, 0)
+    buf = C.create_string_buffer(max(n, 1))
+    call(buf, n)
+    return buf.raw[:n].decode()
+
+
+def deserialize_multi(blob: bytes) -> Runnable:
+    """Rebuild a blob's graph and entries (decode.rs:28-31); raises KuError on a malformed blob."""
+    L = lib()
+    h = L.ku_graph_deserialize(bytes(blob), len(blob))
+    if not h:
+        raise KuError(last_error())
+    try:
+        entries = []
+        for i in range(L.ku_runnable_entry_count(h)):
+            name = _name(lambda out, cap: L.ku_runnable_entry_name(h, i, out, cap))
+            outs = [L.ku_runnable_entry_output(h, i, j) for j in range(L.ku_runnable_entry_output_count(h, i))]
+            ins = []
+            for j in range(L.ku_runnable_entry_input_count(h, i)):
+                nm = _name(lambda out, cap: L.ku_runnable_entry_input_name(h, i, j, out, cap))
+                ins.append(InputBinding(L.ku_runnable_entry_input_node(h, i, j),
+                                        L.ku_runnable_entry_input_role(h, i, j), nm))
+            entries.append(Entry(name, outs, ins))
+        graph = Graph(_handle=L.ku_runnable_take_graph(h))
+    finally:
+        L.ku_runnable_free(h)
+    return Runnable(graph, entries)
+
+
+def deserialize_graph(blob: bytes) -> Runnable:
+    """Same as ``deserialize_multi``; ``outputs``/``inputs`` read entry 0 (decode.rs:20-24)."""
+    return deserialize_multi(blob)
 
 
 def amp_fp8(g: Graph, root: int) -> int:

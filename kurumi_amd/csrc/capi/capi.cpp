@@ -11,6 +11,7 @@
 
 #include "../../../include/kurumi_hip.h"
 #include "../hip/backend.h"
+#include "errors.h"
 #include "handles.h"
 #include "../ir/graph.h"
 #include "../ir/tensor.h"
@@ -23,26 +24,19 @@ struct KuPlan { std::shared_ptr<ku::hipbk::Plan> p; std::vector<NodeId> inputs; 
 struct KuHipPlan { std::unique_ptr<ku::hipbk::Plan> p; ku::hipbk::HipBackend* b; };
 
 namespace {
-
 thread_local std::string g_last_error;
 thread_local bool g_has_error = false;
+}  // namespace
 
-void set_err(const std::string& m) {
+void ku::capi::set_err(const std::string& m) {
   g_last_error = m;
   g_has_error = true;
 }
 
-template <class R, class F>
-R guard(R fail, F&& f) {
-  try {
-    return f();
-  } catch (const std::exception& e) {
-    set_err(e.what());
-  } catch (...) {
-    set_err("unknown error");
-  }
-  return fail;
-}
+namespace {
+
+using ku::capi::guard;
+using ku::capi::set_err;
 
 Shape mk_shape(const size_t* s, size_t rank) {
   if (!s && rank) throw ku::Error("null shape pointer");

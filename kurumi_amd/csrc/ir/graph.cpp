@@ -175,10 +175,15 @@ NodeId Graph::iota(const Shape& shape, size_t axis, DType dt) {
 NodeId Graph::rand_uniform(const Shape& shape, uint64_t seed) {
   int64_t s = static_cast<int64_t>(seed);
   NodeId sn = constant_bytes(DType::I64, reinterpret_cast<const uint8_t*>(&s), 8, {1});
+  return rand_uniform_seeded(shape, sn);
+}
+NodeId Graph::rand_uniform_seeded(const Shape& shape, NodeId seed) {
+  check_id("rand_uniform", seed);
+  if (numel(this->shape(seed)) != 1) throw Error("rand_uniform: seed must hold one element");
   Op op;
   op.kind = OpKind::RandUniform;
   op.shape = shape;
-  return push(std::move(op), {sn});
+  return push(std::move(op), {seed});
 }
 
 NodeId Graph::cast(NodeId a, DType to) {

@@ -93,6 +93,7 @@ class Graph {
   NodeId input(const Shape& shape, DType dt);
   NodeId iota(const Shape& shape, size_t axis, DType dt);
   NodeId rand_uniform(const Shape& shape, uint64_t seed);
+  NodeId rand_uniform_seeded(const Shape& shape, NodeId seed);  // seed: any one-element node
   NodeId cast(NodeId a, DType to);
   NodeId bitcast(NodeId a, DType to);
   NodeId detach(NodeId a);
