@@ -6,9 +6,10 @@ single fused kernel's algorithmic traffic. Every config runs as a device-residen
 (inputs uploaded once, threefry-seeded synthetic data generated on the device), W untimed
 launches, then K timed launches bracketed by stream synchronisation. Per-kernel durations
 come from hipEvents recorded on the plan's own stream. The other configs are reported under
-"configs" with their own roofline fractions.
+"configs" with their own roofline fractions; config "6" is the nn primitives around them
+(rope, the SwiGLU gate, rmsnorm).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -250,6 +251,52 @@ def bench_fp8(hip, steps, warmup):
             "roofline": roofline_mfma(flops, gemm_ms, FP8_PEAK_TFLOPS)}
 
 
+def bench_nn(hip, steps, warmup):
+    """The nn primitives around the configs: rope (f32, the cfg 4 q shape), the SwiGLU gate
+    silu(a) * b (bf16, the cfg 3 MLP shape) and rmsnorm (bf16, the cfg 2 row count). Each is
+    HBM-bound; the gate and rmsnorm run three independent replicas per plan so the working set
+    (3 x 135 MB) exceeds the 256 MB last-level cache, and their time per launch is the plan's
+    GPU time over the replicas."""
+    K = _ku()
+    out = {}
+    shp = [4, 32, 2048, 128]
+    g = K.Graph()
+    feeds, roots = {}, []
+    for r in range(2):  # two replicas: 2 x (134 MB in + 134 MB out) > the last-level cache
+        x = g.input(shp, K.DType.F32)
+        feeds[x] = device_values(hip, scaled_randn(1.0), shp, 401 + r, K.DType.F32)
+        roots.append(g.rope(x))
+    plan = hip.plan(g, roots, feeds)
+    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    main = [i for i, l in enumerate(labels) if l.startswith("ku_ew_4x32x2048x128")]
+    kms = sum(per_step[i] for i in main) / len(main)
+    n = int(np.prod(shp))
+    algo = 8 * n + 2 * 2048 * 64 * 4  # read x, write y, read the two [S, D/2] tables
+    out["nn_rope"] = {"workload": "rope [4,32,2048,128] f32 (table kernel + one fused kernel), 2 replicas per plan",
+                      "ms_per_step": wall_ms / 2, "kernels": labels, "kernel_ms": per_step, "algo_bytes": algo,
+                      "roofline": roofline_hbm(algo, kms, labels[main[0]])}
+    reps = 3
+    for name, shape, build, bytes_per in (
+            ("nn_swiglu", [2048, 11008], lambda gg, ins: gg.mul(gg.silu(ins[0]), ins[1]), 3 * 2),
+            ("nn_rmsnorm", [8192, 4096], lambda gg, ins: gg.rmsnorm(ins[0], 1, 1e-6), 2 * 2)):
+        g = K.Graph()
+        feeds, roots = {}, []
+        for r in range(reps):
+            ins = [g.input(shape, K.DType.BF16) for _ in range(2 if name == "nn_swiglu" else 1)]
+            for i, t in enumerate(ins):
+                feeds[t] = device_values(hip, scaled_randn(2.0), shape, 500 + 10 * r + i, K.DType.BF16)
+            roots.append(build(g, ins))
+        plan = hip.plan(g, roots, feeds)
+        wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+        kms = sum(per_step) / reps
+        algo = bytes_per * int(np.prod(shape))
+        out[name] = {"workload": ("silu(a) * b" if name == "nn_swiglu" else "rmsnorm(x, axis 1, 1e-6)") +
+                     f" {shape} bf16, {reps} independent replicas per plan",
+                     "ms_per_step": wall_ms / reps, "kernels": labels, "kernel_ms": per_step, "algo_bytes": algo,
+                     "roofline": roofline_hbm(algo, kms, labels[0])}
+    return out
+
+
 def bench_copy(hip, steps, warmup):
     """A plain streaming copy of 2^28 f32 (1 GiB read + 1 GiB write) through a one-leaf region."""
     K = _ku()
@@ -269,7 +316,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--configs", default="1,2,3,4,5,6")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--probe-copy", action="store_true",
                     help="also run a plain 1 GiB f32 copy kernel (counter calibration / copy ceiling)")
@@ -306,6 +353,8 @@ def main() -> int:
         extra["cfg4"] = bench_attention(hip, max(3, args.steps // 4), 1)
     if "5" in cfgs:
         extra["cfg5"] = bench_fp8(hip, max(3, args.steps // 4), 1)
+    if "6" in cfgs:
+        extra.update(bench_nn(hip, args.steps, args.warmup))
     if args.probe_copy:
         extra["copy_probe"] = bench_copy(hip, args.steps, args.warmup)
     cpu = None if args.no_cpu else cpu_baseline_cfg2(xt)

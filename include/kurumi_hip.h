@@ -86,6 +86,11 @@ KuNode ku_log2(KuGraph *g, KuNode x);
 KuNode ku_sin(KuGraph *g, KuNode x);
 KuNode ku_cos(KuGraph *g, KuNode x);
 KuNode ku_relu(KuGraph *g, KuNode x);
+KuNode ku_gelu(KuGraph *g, KuNode x);    /* kurumi.h:128 */
+KuNode ku_silu(KuGraph *g, KuNode x);    /* kurumi.h:130 */
+KuNode ku_sigmoid(KuGraph *g, KuNode x); /* kurumi.h:131 */
+KuNode ku_tanh(KuGraph *g, KuNode x);    /* kurumi.h:132 */
+KuNode ku_rope(KuGraph *g, KuNode x);    /* kurumi.h:183 */
 KuNode ku_flatten(KuGraph *g, KuNode x); /* kurumi.h:160 */
 KuNode ku_t(KuGraph *g, KuNode x);       /* kurumi.h:161 */
 KuNode ku_sum_all(KuGraph *g, KuNode x); /* kurumi.h:165 */

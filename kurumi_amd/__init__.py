@@ -176,7 +176,8 @@ def _declare(L: C.CDLL) -> None:
                  "ku_shr", "ku_lt", "ku_eq", "ku_matmul"]:
         sig[name] = ([P, u32, u32], u32)
     for name in ["ku_neg", "ku_recip", "ku_sqrt", "ku_square", "ku_abs", "ku_floor", "ku_exp", "ku_exp2", "ku_ln",
-                 "ku_log2", "ku_sin", "ku_cos", "ku_relu", "ku_detach", "ku_flatten", "ku_t", "ku_sum_all"]:
+                 "ku_log2", "ku_sin", "ku_cos", "ku_relu", "ku_detach", "ku_flatten", "ku_t", "ku_sum_all",
+                 "ku_sigmoid", "ku_silu", "ku_tanh", "ku_gelu", "ku_rope"]:
         sig[name] = ([P, u32], u32)
     for name in ["ku_sum", "ku_prod", "ku_mean", "ku_reduce_max", "ku_argmax", "ku_argmin", "ku_softmax",
                  "ku_squeeze", "ku_unsqueeze"]:
@@ -441,7 +442,9 @@ for _n, _c in [("add", "ku_add"), ("sub", "ku_sub"), ("mul", "ku_mul"), ("div", 
 for _n, _c in [("neg", "ku_neg"), ("recip", "ku_recip"), ("sqrt", "ku_sqrt"), ("square", "ku_square"),
                ("abs", "ku_abs"), ("floor", "ku_floor"), ("exp", "ku_exp"), ("exp2", "ku_exp2"), ("ln", "ku_ln"),
                ("log2", "ku_log2"), ("sin", "ku_sin"), ("cos", "ku_cos"), ("relu", "ku_relu"),
-               ("detach", "ku_detach"), ("flatten", "ku_flatten"), ("t", "ku_t"), ("sum_all", "ku_sum_all")]:
+               ("detach", "ku_detach"), ("flatten", "ku_flatten"), ("t", "ku_t"), ("sum_all", "ku_sum_all"),
+               ("sigmoid", "ku_sigmoid"), ("silu", "ku_silu"), ("tanh", "ku_tanh"), ("gelu", "ku_gelu"),
+               ("rope", "ku_rope")]:
     _add_simple(_n, _c, 1)
 for _n, _c in [("sum", "ku_sum"), ("prod", "ku_prod"), ("mean", "ku_mean"), ("reduce_max", "ku_reduce_max"),
                ("argmax", "ku_argmax"), ("argmin", "ku_argmin"), ("softmax", "ku_softmax"),

@@ -131,6 +131,11 @@ KU_UN(ku_log2, gr.log2(x))
 KU_UN(ku_sin, gr.sin(x))
 KU_UN(ku_cos, gr.cos(x))
 KU_UN(ku_relu, gr.relu(x))
+KU_UN(ku_sigmoid, gr.sigmoid(x))
+KU_UN(ku_silu, gr.silu(x))
+KU_UN(ku_tanh, gr.tanh(x))
+KU_UN(ku_gelu, gr.gelu(x))
+KU_UN(ku_rope, gr.rope(x))
 KU_UN(ku_detach, gr.detach(x))
 KU_UN(ku_flatten, gr.reshape(x, Shape{ku::numel(gr.shape(x))}))
 KU_UN(ku_t, gr.transpose(x, gr.shape(x).size() < 2 ? 0 : gr.shape(x).size() - 2, gr.shape(x).size() < 2 ? 0 : gr.shape(x).size() - 1))

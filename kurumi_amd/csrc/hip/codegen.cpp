@@ -217,7 +217,8 @@ struct Gen {
   // a vectorised bf16 leaf is loaded and kept as packed 32-bit words
   bool bf16_words(int c) const {
     const RNode& cn = node(c);
-    return cn.kind == RK_LEAF && R.leaves[cn.leaf].dtype == DType::BF16 && V % 2 == 0 && leaf_vec[cn.leaf];
+    return cn.kind == RK_LEAF && R.leaves[cn.leaf].dtype == DType::BF16 && V % 2 == 0 && leaf_vec[cn.leaf] &&
+           !R.leaves[cn.leaf].view.padded();
   }
   // 16-bit leaves are cached two to a 32-bit register. (bf16 intermediates could be too -- every
   // bf16 value is carried bf16-exact -- but the pack/unpack VALU cost more than the registers
@@ -327,10 +328,17 @@ void Gen::plan_layout() {
   size_t maxoff = N;
   for (auto& l : R.leaves) {
     int64_t hi = l.view.offset, lo = l.view.offset;
+    bool empty = false;
     for (size_t d = 0; d < l.view.shape.size(); ++d) {
-      int64_t ext = (int64_t)(l.view.shape[d] ? l.view.shape[d] - 1 : 0) * l.view.strides[d];
-      if (ext > 0) hi += ext; else lo += ext;
+      // addressed coordinates: the pad window of a padded view, else the whole axis
+      int64_t c0 = l.view.padded() ? l.view.wlo[d] : 0;
+      int64_t c1 = l.view.padded() ? l.view.whi[d] - 1 : (int64_t)l.view.shape[d] - 1;
+      if (c1 < c0) { empty = true; break; }
+      int64_t a0 = c0 * l.view.strides[d], a1 = c1 * l.view.strides[d];
+      hi += std::max(a0, a1);
+      lo += std::min(a0, a1);
     }
+    if (empty) continue;
     maxoff = std::max<size_t>(maxoff, (size_t)std::max<int64_t>(hi, 0) + 1);
     if (lo < 0) maxoff = std::max<size_t>(maxoff, (size_t)1 << 40);
   }
@@ -353,7 +361,10 @@ void Gen::plan_layout() {
   leaf_vec.assign(R.leaves.size(), false);
   for (size_t i = 0; i < R.leaves.size(); ++i) {
     const View& v = R.leaves[i].view;
-    bool ok = V > 1 && v.strides[vecaxis] == 1 && !v.padded() && (v.offset % V) == 0;
+    // a padded view vectorises when its window on the vector axis is whole vectors (each
+    // vector then lies entirely inside or entirely outside)
+    bool win_ok = !v.padded() || (v.wlo[vecaxis] % V == 0 && v.whi[vecaxis] % V == 0);
+    bool ok = V > 1 && v.strides[vecaxis] == 1 && win_ok && (v.offset % V) == 0;
     for (int d = 0; ok && d < rank; ++d)
       if (d != vecaxis && (v.strides[d] % V) != 0) ok = false;
     leaf_vec[i] = ok;
@@ -490,10 +501,7 @@ std::string Gen::leaf_base(int li) const {
   e << "(" << ix() << ")(" << v.offset << "ll";
   for (int d = 0; d < rank; ++d) {
     if (d == vecaxis || v.strides[d] == 0) continue;
-    int64_t plo = v.padded() ? v.plo[d] : 0;
-    e << " + (i64)(c" << d;
-    if (plo) e << " - " << plo;
-    e << ") * " << v.strides[d] << "ll";
+    e << " + (i64)c" << d << " * " << v.strides[d] << "ll";
   }
   e << ")";
   return e.str();
@@ -514,7 +522,8 @@ void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
     const bool ntl = !flat && (nt_mode() & 2);
     o << "      u32 rw" << ni << "[" << V / 2 << "];\n";
     o << "      { VecT<u32, " << V / 2 << "> raw = " << (ntl ? "vld_nt(" : "*(") << "(const VecT<u32, " << V / 2
-      << ">*)((const " << T << "*)" << P << " + " << base << " + (" << ix() << ")(" << c_expr << ")));\n";
+      << ">*)((const " << T << "*)" << P << " + (" << ix() << ")(" << base << " + (" << ix() << ")(" << c_expr
+      << "))));\n";
     o << "        #pragma unroll\n        for (int jj = 0; jj < " << V / 2 << "; ++jj) rw" << ni << "[jj] = raw.v[jj]; }\n";
     o << "      float f" << ni << "[" << V << "];\n";
     o << "      #pragma unroll\n      for (int jj = 0; jj < " << V / 2 << "; ++jj) { f" << ni
@@ -524,23 +533,30 @@ void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
   }
   // r<ni>: the stored bits (what a leaf cache keeps), f<ni>: the compute values
   o << "      " << T << " r" << ni << "[" << V << "];\n";
-  if (leaf_vec[n.leaf]) {
+  if (leaf_vec[n.leaf] && v.padded()) {
+    std::string coord = "((i64)(" + c_expr + "))";
+    o << "      if (vb" << n.leaf << " && " << coord << " >= " << v.wlo[vecaxis] << " && " << coord << " < "
+      << v.whi[vecaxis] << ") { VecT<" << T << ", " << V << "> raw = *((const VecT<" << T << ", " << V
+      << ">*)((const " << T << "*)" << P << " + (" << ix() << ")(" << base << " + (" << ix() << ")(" << c_expr
+      << "))));\n";
+    o << "        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = raw.v[j];\n";
+    o << "      } else {\n        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = ("
+      << T << ")0;\n      }\n";
+  } else if (leaf_vec[n.leaf]) {
     const bool ntl = !flat && (nt_mode() & 2);
     o << "      { VecT<" << T << ", " << V << "> raw = " << (ntl ? "vld_nt(" : "*(") << "(const VecT<" << T << ", " << V
-      << ">*)((const " << T << "*)" << P << " + " << base << " + (" << ix() << ")(" << c_expr << ")));\n";
+      << ">*)((const " << T << "*)" << P << " + (" << ix() << ")(" << base << " + (" << ix() << ")(" << c_expr
+      << "))));\n";
     o << "        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = raw.v[j]; }\n";
   } else {
     int64_t sa = v.strides[vecaxis];
     o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) {\n";
     std::string coord = "((i64)(" + c_expr + ") + j)";
-    std::string off = base + " + (" + ix() + ")(";
-    if (v.padded()) off += "(" + coord + " - " + std::to_string(v.plo[vecaxis]) + ")";
-    else off += coord;
-    off += " * " + std::to_string(sa) + "ll)";
+    std::string off = base + " + (" + ix() + ")(" + coord + " * " + std::to_string(sa) + "ll)";
     std::string load = "((const " + T + "*)" + P + ")[" + off + "]";
     if (v.padded()) {
-      std::string inr = "(vb" + std::to_string(n.leaf) + " && " + coord + " >= " + std::to_string(v.plo[vecaxis]) +
-                        " && " + coord + " < " + std::to_string(v.plo[vecaxis] + (int64_t)v.src_shape[vecaxis]) + ")";
+      std::string inr = "(vb" + std::to_string(n.leaf) + " && " + coord + " >= " + std::to_string(v.wlo[vecaxis]) +
+                        " && " + coord + " < " + std::to_string(v.whi[vecaxis]) + ")";
       o << "        r" << ni << "[j] = " << inr << " ? " << load << " : (" << T << ")0;\n";
     } else {
       o << "        r" << ni << "[j] = " << load << ";\n";
@@ -582,6 +598,25 @@ void Gen::emit_full_node(int ni, int phase, const std::string& c_expr) {
   }
   if (n.kind == RK_LEAF) {
     emit_leaf_load(ni, c_expr);
+  } else if (n.kind == RK_PADSEL) {
+    // zero outside the pad windows; the non-vector axes are tested once, the vector axis per j
+    int vecaxis = flat ? rank - 1 : a;
+    std::ostringstream cond;
+    cond << "true";
+    for (int d = 0; d < rank; ++d) {
+      if (d == vecaxis) continue;
+      if (n.win.wlo[d] > 0) cond << " && (i64)c" << d << " >= " << n.win.wlo[d];
+      if (n.win.whi[d] < (int64_t)R.S[d]) cond << " && (i64)c" << d << " < " << n.win.whi[d];
+    }
+    std::string cj = "((i64)(" + c_expr + ") + j)";
+    std::ostringstream condj;
+    condj << "pin" << ni;
+    if (n.win.wlo[vecaxis] > 0) condj << " && " << cj << " >= " << n.win.wlo[vecaxis];
+    if (n.win.whi[vecaxis] < (int64_t)R.S[vecaxis]) condj << " && " << cj << " < " << n.win.whi[vecaxis];
+    o << "      const bool pin" << ni << " = " << cond.str() << ";\n";
+    o << "      " << ctype(n.dtype) << " f" << ni << "[" << V << "];\n";
+    o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) f" << ni << "[j] = (" << condj.str()
+      << ") ? " << val(n.in[0], "j") << " : (" << ctype(n.dtype) << ")0;\n";
   } else if (n.kind == (int)OpKind::Iota || n.kind == (int)OpKind::RandUniform) {
     int vecaxis = flat ? rank - 1 : a;
     o << "      " << ctype(n.dtype) << " f" << ni << "[" << V << "];\n";
@@ -831,13 +866,16 @@ std::string Gen::generate(RegionCode* rc) {
   }
   // leaf bases (+ padding validity on the non-vector axes)
   for (size_t li = 0; li < R.leaves.size(); ++li) {
+    // b<leaf> is the element index modulo the index width: a padded view's offset may lie before
+    // the buffer, so the vector-axis term is always added in the index type before the pointer
     o << "  const " << ix() << " b" << li << " = " << leaf_base((int)li) << ";\n";
     const View& v = R.leaves[li].view;
     if (v.padded()) {
       o << "  const bool vb" << li << " = true";
       for (int d = 0; d < rank; ++d) {
         if (d == vecaxis) continue;
-        o << " && (i64)c" << d << " >= " << v.plo[d] << " && (i64)c" << d << " < " << v.plo[d] + (int64_t)v.src_shape[d];
+        if (v.wlo[d] > 0) o << " && (i64)c" << d << " >= " << v.wlo[d];
+        if (v.whi[d] < (int64_t)v.shape[d]) o << " && (i64)c" << d << " < " << v.whi[d];
       }
       o << ";\n";
     }

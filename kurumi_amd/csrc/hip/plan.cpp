@@ -33,9 +33,39 @@ bool View::is_contiguous() const {
   return true;
 }
 
+// A padded view reshapes without a copy only when the reshape inserts or drops unit axes
+// (every windowed axis keeps its extent and window).
+static bool view_reshape_padded(const View& v, const Shape& to, View* out) {
+  View r;
+  r.shape = to;
+  r.offset = v.offset;
+  size_t oi = 0;
+  for (size_t ni = 0; ni < to.size(); ++ni) {
+    while (oi < v.shape.size() && v.shape[oi] == 1) {  // dropped unit axis: must be inside its window
+      if (!(v.wlo[oi] <= 0 && 0 < v.whi[oi])) return false;
+      ++oi;
+    }
+    if (to[ni] == 1) {
+      r.strides.push_back(0);
+      r.wlo.push_back(0);
+      r.whi.push_back(1);
+      continue;
+    }
+    if (oi >= v.shape.size() || v.shape[oi] != to[ni]) return false;
+    r.strides.push_back(v.strides[oi]);
+    r.wlo.push_back(v.wlo[oi]);
+    r.whi.push_back(v.whi[oi]);
+    ++oi;
+  }
+  for (; oi < v.shape.size(); ++oi)
+    if (v.shape[oi] != 1 || !(v.wlo[oi] <= 0 && 0 < v.whi[oi])) return false;
+  *out = r;
+  return true;
+}
+
 // No-copy reshape (dims grouped by equal products; each old group must be dense).
 bool view_reshape(const View& v, const Shape& to, View* out) {
-  if (v.padded()) return false;
+  if (v.padded()) return view_reshape_padded(v, to, out);
   if (numel(v.shape) == 0) {
     *out = View::contiguous(to);
     out->offset = v.offset;
@@ -82,7 +112,14 @@ View view_expand(const View& v, const Shape& to) {
   View r = v;
   r.shape = to;
   for (size_t i = 0; i < to.size(); ++i)
-    if (v.shape[i] == 1 && to[i] != 1) r.strides[i] = 0;
+    if (v.shape[i] == 1 && to[i] != 1) {
+      r.strides[i] = 0;
+      if (v.padded()) {  // the one source element is either inside its window or not
+        bool in = v.wlo[i] <= 0 && 0 < v.whi[i];
+        r.wlo[i] = 0;
+        r.whi[i] = in ? (int64_t)to[i] : 0;
+      }
+    }
   return r;
 }
 
@@ -92,16 +129,30 @@ View view_permute(const View& v, const std::vector<size_t>& perm) {
   for (size_t p : perm) {
     r.shape.push_back(v.shape[p]);
     r.strides.push_back(v.strides[p]);
+    if (v.padded()) {
+      r.wlo.push_back(v.wlo[p]);
+      r.whi.push_back(v.whi[p]);
+    }
   }
   return r;
+}
+
+static int64_t ceil_div(int64_t a, int64_t b) {  // b > 0
+  return a >= 0 ? (a + b - 1) / b : -((-a) / b);
 }
 
 View view_slice(const View& v, const std::vector<SliceRange>& rg) {
   View r = v;
   for (size_t i = 0; i < rg.size(); ++i) {
-    r.offset += (int64_t)rg[i].start * v.strides[i];
-    r.strides[i] = v.strides[i] * (int64_t)rg[i].step;
+    int64_t start = (int64_t)rg[i].start, step = (int64_t)rg[i].step;
+    r.offset += start * v.strides[i];
+    r.strides[i] = v.strides[i] * step;
     r.shape[i] = (rg[i].end - rg[i].start + rg[i].step - 1) / rg[i].step;
+    if (v.padded()) {  // new c valid iff wlo <= start + c*step < whi
+      int64_t n = (int64_t)r.shape[i];
+      r.wlo[i] = std::min(std::max<int64_t>(ceil_div(v.wlo[i] - start, step), 0), n);
+      r.whi[i] = std::min(std::max<int64_t>(ceil_div(v.whi[i] - start, step), 0), n);
+    }
   }
   return r;
 }
@@ -110,26 +161,36 @@ View view_flip(const View& v, const std::vector<size_t>& axes) {
   View r = v;
   for (size_t a : axes) {
     if (r.shape[a] == 0) continue;
-    r.offset += (int64_t)(r.shape[a] - 1) * r.strides[a];
+    int64_t n = (int64_t)r.shape[a];
+    r.offset += (n - 1) * r.strides[a];
     r.strides[a] = -r.strides[a];
+    if (r.padded()) {  // c' = n-1-c: valid iff n - whi <= c' < n - wlo
+      int64_t lo = n - r.whi[a], hi = n - r.wlo[a];
+      r.wlo[a] = lo;
+      r.whi[a] = hi;
+    }
   }
   return r;
 }
 
 View view_pad(const View& v, const std::vector<PadRange>& p) {
   View r = v;
-  r.src_shape = v.shape;
-  r.plo.resize(p.size());
+  if (!r.padded()) {
+    r.wlo.assign(v.shape.size(), 0);
+    r.whi.assign(v.shape.begin(), v.shape.end());
+  }
   for (size_t i = 0; i < p.size(); ++i) {
-    r.plo[i] = (int64_t)p[i].lo;
+    int64_t lo = (int64_t)p[i].lo;
+    r.offset -= lo * v.strides[i];
+    r.wlo[i] += lo;
+    r.whi[i] += lo;
     r.shape[i] = p[i].lo + v.shape[i] + p[i].hi;
   }
   return r;
 }
 
 static bool view_eq(const View& a, const View& b) {
-  return a.shape == b.shape && a.strides == b.strides && a.offset == b.offset && a.plo == b.plo &&
-         a.src_shape == b.src_shape;
+  return a.shape == b.shape && a.strides == b.strides && a.offset == b.offset && a.wlo == b.wlo && a.whi == b.whi;
 }
 
 // ======================= const cache =======================
@@ -279,6 +340,7 @@ class Planner {
   void visit(NodeId id);
   void visit_elementwise(NodeId id);
   void visit_movement(NodeId id);
+  bool clone_through_movement(NodeId id);
   void visit_reduce(NodeId id);
   void visit_rowop(NodeId id);
   void visit_dot(NodeId id);
@@ -557,9 +619,100 @@ void Planner::visit_elementwise(NodeId id) {
   vals_[id] = v;
 }
 
+// The moved view of `v` for movement node `n` (false when a reshape needs a copy).
+static bool move_view(const Node& n, const View& v, View* out) {
+  switch (n.op.kind) {
+    case OpKind::Reshape: return view_reshape(v, n.shape, out);
+    case OpKind::Expand: *out = view_expand(v, n.shape); return true;
+    case OpKind::Permute: *out = view_permute(v, n.op.perm); return true;
+    case OpKind::Slice: *out = view_slice(v, n.op.ranges); return true;
+    case OpKind::Flip: *out = view_flip(v, n.op.axes); return true;
+    case OpKind::Pad: *out = view_pad(v, n.op.pads); return true;
+    default: return false;
+  }
+}
+
+// A movement of a lazy elementwise value becomes the same expression evaluated in the moved
+// coordinates: its nodes are cloned into a region of the output shape with every leaf view
+// (and every pad window) moved the same way, so no buffer and no kernel boundary appear. A
+// Pad adds a select that zeroes the new border. Not done when the expression depends on its
+// own coordinates (iota, rand), lives in a reduction region, or when a broadcast would
+// repeat real work per output element (that value is computed once instead).
+bool Planner::clone_through_movement(NodeId id) {
+  const Node& n = g_.node(id);
+  NodeId s = n.src[0];
+  const Val a = vals_[s];
+  if (a.k != Val::LFull) return false;
+  const int srid = a.region;
+  if (P_.regions_[srid].axis >= 0 || P_.regions_[srid].S != g_.shape(s)) return false;
+  std::vector<RNode> nodes = P_.regions_[srid].nodes;
+  std::vector<Leaf> leaves = P_.regions_[srid].leaves;
+  std::vector<int> order;
+  std::vector<char> seen(nodes.size(), 0);
+  std::function<void(int)> walk = [&](int i) {
+    if (seen[i]) return;
+    seen[i] = 1;
+    for (int j : nodes[i].in) walk(j);
+    order.push_back(i);
+  };
+  walk(a.rn);
+  int heavy = 0;
+  for (int i : order) {
+    const RNode& rn = nodes[i];
+    if (rn.kind == RK_LEAF || rn.kind == RK_PADSEL) continue;
+    if (rn.kind >= RK_LEAF || !is_elementwise((OpKind)rn.kind)) return false;
+    switch ((OpKind)rn.kind) {
+      case OpKind::Exp2: case OpKind::Log2: case OpKind::Sin: case OpKind::Sqrt: case OpKind::Recip:
+      case OpKind::IDiv:
+        ++heavy;
+        break;
+      default: break;
+    }
+  }
+  if (n.op.kind == OpKind::Expand && numel(n.shape) > numel(g_.shape(s)) && (heavy > 0 || order.size() > 12))
+    return false;
+  std::vector<View> moved(nodes.size());
+  for (int i : order) {
+    const RNode& rn = nodes[i];
+    if (rn.kind == RK_LEAF && !move_view(n, leaves[rn.leaf].view, &moved[i])) return false;
+    if (rn.kind == RK_PADSEL && !move_view(n, rn.win, &moved[i])) return false;
+  }
+  int rid = new_region(n.shape);
+  std::vector<int> map(nodes.size(), -1);
+  for (int i : order) {
+    const RNode& rn = nodes[i];
+    if (rn.kind == RK_LEAF) {
+      map[i] = add_leaf(rid, leaves[rn.leaf].slot, moved[i], leaves[rn.leaf].dtype);
+      continue;
+    }
+    RNode c = rn;
+    c.space = Space::Full;
+    for (int& j : c.in) j = map[j];
+    if (rn.kind == RK_PADSEL) c.win = moved[i];
+    map[i] = add_node(rid, c);
+  }
+  int root = map[a.rn];
+  if (n.op.kind == OpKind::Pad) {
+    RNode ps;
+    ps.kind = RK_PADSEL;
+    ps.dtype = nodes[a.rn].dtype;
+    ps.space = Space::Full;
+    ps.in = {root};
+    ps.win = view_pad(View::contiguous(g_.shape(s)), n.op.pads);
+    root = add_node(rid, ps);
+  }
+  Val v;
+  v.k = Val::LFull;
+  v.region = rid;
+  v.rn = root;
+  vals_[id] = v;
+  return true;
+}
+
 void Planner::visit_movement(NodeId id) {
   const Node& n = g_.node(id);
   NodeId s = n.src[0];
+  if (vals_[s].k == Val::LFull && clone_through_movement(id)) return;
   Val& a = vals_[s];
   if (a.k != Val::Dev) {
     Region& R = P_.regions_[a.region];
@@ -590,10 +743,6 @@ void Planner::visit_movement(NodeId id) {
   Val& d = vals_[s];
   View v = d.view;
   int slot = d.slot;
-  if (v.padded() && n.op.kind != OpKind::Reshape) {
-    slot = copy_view_to_slot(v, slot, n.dtype, s);
-    v = View::contiguous(g_.shape(s));
-  }
   View r;
   switch (n.op.kind) {
     case OpKind::Reshape:
@@ -764,6 +913,15 @@ void Planner::visit_dot(NodeId id) {
   }
   View av = dev_view_of(an), bv = dev_view_of(bn);
   int aslot = vals_[an].slot, bslot = vals_[bn].slot;
+  // the GEMM kernels read plain strided operands: zero-padded views are copied out first
+  if (av.padded()) {
+    aslot = copy_view_to_slot(av, aslot, g_.dtype(an), an);
+    av = View::contiguous(av.shape);
+  }
+  if (bv.padded()) {
+    bslot = copy_view_to_slot(bv, bslot, g_.dtype(bn), bn);
+    bv = View::contiguous(bv.shape);
+  }
   DType in_dt = g_.dtype(an);
   const Op& op = n.op;
   std::vector<size_t> afree = free_axes(av.shape.size(), op.lb, op.lc);
@@ -1212,8 +1370,8 @@ void Planner::run() {
     P_.order_.push_back(s);
   };
   for (int s = 0; s < ns; ++s)
-    if (step_alive_[s] && (P_.steps_[s].type != Step::REGION || !P_.regions_[P_.steps_[s].index].nodes.empty()))
-      dfs(s);
+    if (step_alive_[s] && (P_.steps_[s].type != Step::REGION || !P_.regions_[P_.steps_[s].index].outputs.empty()))
+      dfs(s);  // a region nobody reads (its values were all moved into other regions) is not run
 }
 
 // ======================= plan =======================

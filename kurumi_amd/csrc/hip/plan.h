@@ -27,11 +27,13 @@ struct View {
   Shape shape;
   std::vector<int64_t> strides;
   int64_t offset = 0;
-  // zero padding (Pad): coordinate c on axis d reads source c - plo[d] when inside
-  // [0, src_shape[d]), else 0. Empty when the view is not padded.
-  std::vector<int64_t> plo;
-  Shape src_shape;
-  bool padded() const { return !plo.empty(); }
+  // zero padding (Pad): element c reads offset + sum(c[d] * strides[d]) when every coordinate
+  // lies in its window wlo[d] <= c[d] < whi[d], else 0. Windows are in this view's own
+  // coordinates, so pads compose with slices, flips, permutes, expands and further pads; the
+  // offset may point before the buffer (only valid coordinates are ever read). Empty when the
+  // view is not padded.
+  std::vector<int64_t> wlo, whi;
+  bool padded() const { return !wlo.empty(); }
   static View contiguous(const Shape& s);
   bool is_contiguous() const;
 };
@@ -61,6 +63,7 @@ enum RK : int {
   RK_DIV,            // a / b (f32/f64 division, Softmax/RmsNorm)
   RK_EXP,            // natural exp (Softmax)
   RK_SQRT_ADD_EPS,   // sqrt(a / len + eps) (RmsNorm)
+  RK_PADSEL,         // in[0] where the coordinate lies in the windows of `win`, else 0 (Pad)
 };
 
 struct RNode {
@@ -74,6 +77,7 @@ struct RNode {
   size_t axis = 0;            // Iota axis
   float eps = 0.f;
   int level = 0;
+  View win;                   // RK_PADSEL: only its wlo/whi windows are used
 };
 
 struct Leaf {

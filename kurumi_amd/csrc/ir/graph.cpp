@@ -378,6 +378,106 @@ NodeId Graph::cos(NodeId a) {
   return sin(s);
 }
 
+NodeId Graph::tanh(NodeId a) {
+  NodeId two = scalar(a, 2.0f);
+  NodeId x2 = mul(a, two);
+  NodeId s = sigmoid(x2);
+  NodeId two2 = scalar(a, 2.0f);
+  NodeId s2 = mul(s, two2);
+  NodeId one = scalar(a, 1.0f);
+  return sub(s2, one);
+}
+NodeId Graph::sigmoid(NodeId a) {
+  NodeId na = neg(a);
+  NodeId e = exp(na);
+  NodeId one = scalar(a, 1.0f);
+  NodeId d = add(one, e);
+  return recip(d);
+}
+NodeId Graph::silu(NodeId a) {
+  NodeId s = sigmoid(a);
+  return mul(a, s);
+}
+NodeId Graph::gelu(NodeId a) {
+  NodeId x2 = mul(a, a);
+  NodeId x3 = mul(x2, a);
+  NodeId c = scalar(a, 0.044715f);
+  NodeId cx3 = mul(c, x3);
+  NodeId inner = add(a, cx3);
+  NodeId k = scalar(a, std::sqrt(2.0f / 3.14159265358979323846f));  // (2/pi).sqrt() in f32
+  NodeId scaled = mul(k, inner);
+  NodeId t = tanh(scaled);
+  NodeId one = scalar(a, 1.0f);
+  NodeId onep = add(one, t);
+  NodeId half = scalar(a, 0.5f);
+  NodeId hx = mul(half, a);
+  return mul(hx, onep);
+}
+
+// attention.rs:9-36: x*cos + rotate_half(x)*sin over [.., S, D], angle[s,i] = s * 10000^(-2i/D),
+// with cos = sin(angle + pi/2) and the tables built in f32 from two iotas.
+NodeId Graph::rope(NodeId x) {
+  check_id("rope", x);
+  Shape xs = shape(x);
+  size_t r = xs.size();
+  if (r < 2) throw Error("rope: rank >= 2 required, got " + shape_str(xs));
+  size_t s = xs[r - 2], d = xs[r - 1], half = d / 2;
+  NodeId pos = iota({s, half}, 0, DType::F32);
+  NodeId fi = iota({s, half}, 1, DType::F32);
+  const float ln10000 = 9.21034049987792969f;  // 10000f32.ln(), the f32 nearest ln(10^4)
+  NodeId c = scalar(fi, -2.0f * ln10000 / static_cast<float>(d));
+  NodeId ic = mul(fi, c);
+  NodeId theta = exp(ic);
+  NodeId angle = mul(pos, theta);
+  NodeId sin_h = sin(angle);
+  NodeId hp = scalar(angle, 1.57079632679489661923f);  // FRAC_PI_2
+  NodeId cos_arg = add(angle, hp);
+  NodeId cos_h = sin(cos_arg);
+  NodeId cos_full = concat_last(cos_h, cos_h, half);
+  NodeId sin_full = concat_last(sin_h, sin_h, half);
+  NodeId x1 = slice_last(x, 0, half);
+  NodeId x2 = slice_last(x, half, d);
+  NodeId nx2 = neg(x2);
+  NodeId rot = concat_last(nx2, x1, half);
+  NodeId cos_b = broadcast_2d_to(cos_full, xs);
+  NodeId sin_b = broadcast_2d_to(sin_full, xs);
+  NodeId a = mul(x, cos_b);
+  NodeId b = mul(rot, sin_b);
+  return add(a, b);
+}
+
+// attention.rs:39-50: [.., La] ++ [.., Lb] on the last axis as pad(a, right Lb) + pad(b, left La).
+NodeId Graph::concat_last(NodeId a, NodeId b, size_t alen) {
+  size_t r = shape(a).size();
+  size_t blen = shape(b)[r - 1];
+  std::vector<PadRange> pa(r, {0, 0}), pb(r, {0, 0});
+  pa[r - 1] = {0, blen};
+  pb[r - 1] = {alen, 0};
+  NodeId ap = pad(a, pa);
+  NodeId bp = pad(b, pb);
+  return add(ap, bp);
+}
+
+// attention.rs:53-59
+NodeId Graph::slice_last(NodeId a, size_t start, size_t end) {
+  const Shape& sh = shape(a);
+  std::vector<SliceRange> rg;
+  for (size_t dim : sh) rg.push_back({0, dim, 1});
+  rg.back() = {start, end, 1};
+  return slice(a, rg);
+}
+
+// attention.rs:62-70: [A, B] -> [1, .., 1, A, B] -> target
+NodeId Graph::broadcast_2d_to(NodeId t, const Shape& target) {
+  const Shape& ts = shape(t);
+  size_t r = target.size();
+  Shape full(r, 1);
+  full[r - 2] = ts[0];
+  full[r - 1] = ts[1];
+  NodeId tr = reshape(t, full);
+  return expand(tr, target);
+}
+
 // random.rs:28-40 (Box-Muller over the `seed` and `seed ^ 0xD1B54A32D192ED03` streams)
 NodeId Graph::randn(const Shape& shape, uint64_t seed) {
   NodeId u1 = rand_uniform(shape, seed);

@@ -128,6 +128,11 @@ class Graph {
   NodeId relu(NodeId a);            // activation.rs:17-20
   NodeId square(NodeId a);
   NodeId cos(NodeId a);             // trig.rs: sin(x + pi/2)
+  NodeId tanh(NodeId a);            // trig.rs:50-58: 2*sigmoid(2x) - 1
+  NodeId sigmoid(NodeId a);         // activation.rs:8-14
+  NodeId silu(NodeId a);            // activation.rs:23-26
+  NodeId gelu(NodeId a);            // activation.rs:29-44 (tanh form)
+  NodeId rope(NodeId a);            // attention.rs:9-36 (NeoX rotate-half, base 10000)
   NodeId randn(const Shape& shape, uint64_t seed);                    // random.rs:28-40
   NodeId rand_range(const Shape& shape, uint64_t seed, float lo, float hi);  // random.rs:43-49
   NodeId mean(NodeId a, size_t axis);
@@ -173,6 +178,9 @@ class Graph {
   DType infer_dtype(const Op& op, const std::vector<NodeId>& src) const;
   Shape derive_shape(const Op& op, const std::vector<NodeId>& src) const;
   NodeId causal_bias(size_t s, const Shape& out_shape);
+  NodeId concat_last(NodeId a, NodeId b, size_t alen);
+  NodeId slice_last(NodeId a, size_t start, size_t end);
+  NodeId broadcast_2d_to(NodeId t, const Shape& target);
 
   std::vector<Node> nodes_;
   uint64_t id_;

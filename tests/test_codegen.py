@@ -138,3 +138,64 @@ def test_unsupported_dtype_is_an_error_not_a_fallback():
     y = g.add(z, z)
     with pytest.raises(K.KuError, match="complex"):
         g.codegen([y])
+
+
+# ---------------- movement through computed values, nn chains ----------------
+
+def test_rope_is_one_table_kernel_and_one_fused_kernel():
+    """rope (attention.rs:9-36): the [S, D/2] angle table is computed once, everything else --
+    two half slices, the negation, both pad+add concats and the broadcast tables -- is one pass."""
+    g = Graph()
+    x = g.input([4, 32, 2048, 128], DType.F32)
+    st = steps(g.codegen([g.rope(x)], compile=True))
+    assert len(st) == 2, st
+    assert st[0].startswith("ku_ew_2048x64_") and st[1].startswith("ku_ew_4x32x2048x128_")
+
+
+def test_movement_of_computed_values_stays_in_one_kernel():
+    g = Graph()
+    x = g.input([64, 96], DType.F32)
+    y = g.input([96, 64], DType.F32)
+    t = g.add(g.transpose(g.neg(x), 0, 1), y)                        # permute of a computed value
+    p = g.pad(g.exp(x), [(1, 2), (0, 4)])                            # pad of a computed value
+    c = g.add(g.pad(g.neg(x), [(0, 0), (0, 96)]), g.pad(g.exp(x), [(0, 0), (96, 0)]))  # concat
+    f = g.flip(g.slice_step(g.mul(x, x), [(0, 64, 2), (3, 96, 1)]), [0, 1])
+    for root in (t, p, c, f):
+        st = steps(g.codegen([root], compile=True))
+        assert len(st) == 1, (root, st)
+
+
+def test_broadcast_of_costly_values_is_computed_once():
+    g = Graph()
+    v = g.input([256], DType.F32)
+    big = g.add(g.broadcast_to(g.exp(v), [512, 256]), g.input([512, 256], DType.F32))
+    assert len(steps(g.codegen([big]))) == 2
+    cheap = g.add(g.broadcast_to(g.neg(v), [512, 256]), g.input([512, 256], DType.F32))
+    assert len(steps(g.codegen([cheap]))) == 1
+
+
+@pytest.mark.parametrize("act", ["silu", "gelu", "sigmoid", "tanh"])
+@pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
+def test_activation_chains_are_one_kernel(act, dt):
+    g = Graph()
+    a = g.input([2048, 11008], dt)
+    b = g.input([2048, 11008], dt)
+    y = g.mul(getattr(g, act)(a), b)  # e.g. the SwiGLU gate silu(a) * b
+    st = steps(g.codegen([y], compile=True))
+    assert len(st) == 1 and st[0].startswith("ku_ew_2048x11008_"), st
+
+
+@pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
+def test_rmsnorm_is_one_line_kernel(dt):
+    g = Graph()
+    x = g.input([8192, 4096], dt)
+    st = steps(g.codegen([g.rmsnorm(x, 1, 1e-6)], compile=True))
+    assert len(st) == 1 and st[0].startswith("ku_line_8192x4096_"), st
+
+
+def test_rope_rejects_bf16_like_the_reference():
+    """The rope tables are f32 (attention.rs:14-15), so `mul(x, cos)` needs an f32 x."""
+    g = Graph()
+    x = g.input([2, 8, 16], DType.BF16)
+    with pytest.raises(K.KuError, match="dtype"):
+        g.rope(x)
