@@ -184,6 +184,48 @@ struct Gen {
   }
   const RNode& node(int i) const { return R.nodes[i]; }
   bool full(int i) const { return R.nodes[i].space == Space::Full; }
+  // An f32 division by a line value whose every consumer rounds to a 16- or 8-bit float:
+  // computed as x * (1 / d) with the reciprocal taken once per line. The product differs from
+  // the quotient by at most one f32 ulp, which moves the narrow result only when it lies
+  // within 2^-24 of a rounding boundary (1 narrow ulp then).
+  bool div_by_line_recip(int ni) const {
+    const RNode& n = R.nodes[ni];
+    if (n.kind != RK_DIV || n.dtype != DType::F32 || flat || full(n.in[1])) return false;
+    bool any = false;
+    for (size_t i = 0; i < R.nodes.size(); ++i)
+      for (int j : R.nodes[i].in)
+        if (j == ni) {
+          const RNode& c = R.nodes[i];
+          if (c.kind != (int)OpKind::Cast || !dt_is_lowp(c.to)) return false;
+          any = true;
+        }
+    for (auto& op : R.outputs)
+      if (op.first == ni) return false;
+    return any;
+  }
+  // Every consumer of node ni is IEEE arithmetic that turns a signalling NaN operand into the
+  // same quiet NaN by itself (and ni is not stored), so a widening cast need not quiet first.
+  bool consumers_quiet(int ni) const {
+    for (auto& op : R.outputs)
+      if (op.first == ni) return false;
+    for (size_t i = 0; i < R.nodes.size(); ++i)
+      for (int j : R.nodes[i].in)
+        if (j == ni) {
+          int k = R.nodes[i].kind;
+          bool q = k == (int)OpKind::Add || k == (int)OpKind::Mul || k == (int)OpKind::Recip ||
+                   k == (int)OpKind::Sqrt || k == (int)OpKind::Exp2 || k == (int)OpKind::Log2 ||
+                   k == (int)OpKind::Sin || k == (int)OpKind::Floor || k == (int)OpKind::Sum ||
+                   k == (int)OpKind::Prod || k == RK_DIV || k == RK_EXP || k == RK_SQRT_ADD_EPS ||
+                   (k == (int)OpKind::Cast && (R.nodes[i].to == DType::BF16 || R.nodes[i].to == DType::F16));
+          if (!q) return false;
+        }
+    return true;
+  }
+  bool needs_line_recip(int li) const {
+    for (size_t i = 0; i < R.nodes.size(); ++i)
+      if (R.nodes[i].kind == RK_DIV && R.nodes[i].in[1] == li && div_by_line_recip((int)i)) return true;
+    return false;
+  }
   std::string ix() const { return idx64 ? "u64" : "u32"; }
 
   // value of node i at element j (FULL) or as a line scalar (LINE)
@@ -218,7 +260,7 @@ struct Gen {
   bool bf16_words(int c) const {
     const RNode& cn = node(c);
     return cn.kind == RK_LEAF && R.leaves[cn.leaf].dtype == DType::BF16 && V % 2 == 0 && leaf_vec[cn.leaf] &&
-           !R.leaves[cn.leaf].view.padded();
+           !R.leaves[cn.leaf].view.padded() && !R.leaves[cn.leaf].imm;
   }
   // 16-bit leaves are cached two to a 32-bit register. (bf16 intermediates could be too -- every
   // bf16 value is carried bf16-exact -- but the pack/unpack VALU cost more than the registers
@@ -275,7 +317,13 @@ std::string Gen::op_expr(int ni, const std::string& j) const {
     case (int)OpKind::Neg:
       if (fl || f64) return "(-" + in(0) + ")";
       return "(" + T + ")(0 - (" + U + ")" + in(0) + ")";
-    case (int)OpKind::Recip: return f64 ? "(1.0 / " + in(0) + ")" : rnd(d, "(1.0f / " + in(0) + ")");
+    case (int)OpKind::Recip:
+      if (f64) return "(1.0 / " + in(0) + ")";
+      // per-element results rounded to 16 or 8 bits right away: v_rcp_f32 (1 ulp) instead of the
+      // correctly rounded f32 division, as for exp2 below (a once-per-line value keeps the division)
+      if (n.space == Space::Full && (d == DType::BF16 || d == DType::F16 || d == DType::F8E4M3 || d == DType::F8E5M2))
+        return rnd(d, "__builtin_amdgcn_rcpf(" + in(0) + ")");
+      return rnd(d, "(1.0f / " + in(0) + ")");
     case (int)OpKind::Sqrt: return f64 ? "sqrt(" + in(0) + ")" : rnd(d, "sqrtf(" + in(0) + ")");
     case (int)OpKind::Exp2:
       if (f64) return "exp2(" + in(0) + ")";
@@ -301,14 +349,18 @@ std::string Gen::op_expr(int ni, const std::string& j) const {
     case (int)OpKind::CmpLt: return "(" + in(0) + " < " + in(1) + ")";
     case (int)OpKind::CmpEq: return "(" + in(0) + " == " + in(1) + ")";
     case (int)OpKind::Where: return "(" + in(0) + " ? " + in(1) + " : " + in(2) + ")";
-    case (int)OpKind::Cast: return cast_expr(indt(0), n.to, in(0));
+    case (int)OpKind::Cast:
+      if (n.to == DType::F32 && dt_is_lowp(indt(0)) && consumers_quiet(ni)) return in(0);
+      return cast_expr(indt(0), n.to, in(0));
     case (int)OpKind::Bitcast: {
       DType s = indt(0);
       std::string raw = std::string("__builtin_bit_cast(") + stype(n.to) + ", (" + stype(s) + ")" + st(s, in(0)) + ")";
       if (s == DType::BOOL || n.to == DType::BOOL) raw = std::string("(") + stype(n.to) + ")" + st(s, in(0));
       return ld(n.to, raw);
     }
-    case RK_DIV: return "(" + in(0) + " / " + in(1) + ")";
+    case RK_DIV:
+      if (div_by_line_recip(ni)) return "(" + in(0) + " * s" + std::to_string(n.in[1]) + "_inv)";
+      return "(" + in(0) + " / " + in(1) + ")";
     case RK_EXP: return f64 ? "exp(" + in(0) + ")" : "expf(" + in(0) + ")";
     case RK_SQRT_ADD_EPS: {
       std::string len = flt_lit(d, (double)n.axis), eps = flt_lit(d, (double)n.eps);
@@ -494,6 +546,15 @@ void Gen::schedule() {
   }
 }
 
+// The stored bits of an immediate constant leaf as a value of its storage type.
+static std::string imm_expr(const Leaf& l) {
+  size_t w = dt_width(l.dtype);
+  const char* U = w == 1 ? "u8" : w == 2 ? "u16" : w == 4 ? "u32" : "u64";
+  std::ostringstream e;
+  e << "__builtin_bit_cast(" << stype(l.dtype) << ", (" << U << ")0x" << std::hex << l.imm_bits[0] << "ull)";
+  return e.str();
+}
+
 std::string Gen::leaf_base(int li) const {
   const View& v = R.leaves[li].view;
   int vecaxis = flat ? rank - 1 : a;
@@ -516,6 +577,12 @@ void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
   std::string T = stype(l.dtype), C = ctype(l.dtype);
   std::string P = "p" + std::to_string(slot_param.at(l.slot));
   std::string base = "b" + std::to_string(n.leaf);
+  if (l.imm) {
+    o << "      " << T << " r" << ni << "[" << V << "];\n";
+    o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = " << imm_expr(l) << ";\n";
+    emit_leaf_convert(ni);
+    return;
+  }
   if (bf16_words(ni)) {
     // bf16 pairs stay packed in 32-bit words (the form the cache keeps); each value is its word's
     // low half shifted up or its high half masked
@@ -683,10 +750,13 @@ void Gen::emit_line_node(int ni) {
   if (n.kind == RK_LEAF) {
     const Leaf& l = R.leaves[n.leaf];
     std::string P = "p" + std::to_string(slot_param.at(l.slot));
-    o << "  const " << ctype(n.dtype) << " s" << ni << " = " << ld(l.dtype, "((const " + std::string(stype(l.dtype)) + "*)" + P + ")[b" + std::to_string(n.leaf) + "]") << ";\n";
+    std::string raw = l.imm ? imm_expr(l)
+                            : "((const " + std::string(stype(l.dtype)) + "*)" + P + ")[b" + std::to_string(n.leaf) + "]";
+    o << "  const " << ctype(n.dtype) << " s" << ni << " = " << ld(l.dtype, raw) << ";\n";
   } else {
     o << "  const " << ctype(n.dtype) << " s" << ni << " = " << op_expr(ni, "0") << ";\n";
   }
+  if (needs_line_recip(ni)) o << "  const float s" << ni << "_inv = 1.0f / s" << ni << ";\n";
   auto it = out_slot.find(ni);
   if (it != out_slot.end() && !full(ni) && !flat) {
     o << "  if (lane == 0) ((" << stype(n.dtype) << "*)p" << slot_param.at(it->second) << ")[line] = "
@@ -814,6 +884,7 @@ void Gen::emit_red_finish(int ni, int phase) {
     if (dt_is_int(n.dtype)) v = std::string("(") + stype(n.dtype) + ")" + v;
     else v = rnd(n.dtype, v);
     o << "  const " << ctype(n.dtype) << " s" << r << " = " << v << ";\n";
+    if (needs_line_recip(ni)) o << "  const float s" << r << "_inv = 1.0f / s" << r << ";\n";
   }
   auto it = out_slot.find(ni);
   if (it != out_slot.end()) {
@@ -897,7 +968,12 @@ std::string Gen::generate(RegionCode* rc) {
       const RNode& n = node(op.first);
       std::string T = stype(n.dtype);
       std::string P = "p" + std::to_string(slot_param.at(op.second));
-      if (V > 1) {
+      if (V > 1 && n.dtype == DType::BF16 && V % 2 == 0 && n.kind != RK_LEAF) {
+        // every bf16 op result is already bf16-exact: pack pairs with one v_perm each
+        o << "    { VecT<u32, " << V / 2 << "> w;\n      #pragma unroll\n      for (int jj = 0; jj < " << V / 2
+          << "; ++jj) w.v[jj] = pack_bf16_exact(f" << op.first << "[2 * jj], f" << op.first << "[2 * jj + 1]);\n"
+          << "      *(VecT<u32, " << V / 2 << ">*)((" << T << "*)" << P << " + chunk * " << V << "ull) = w; }\n";
+      } else if (V > 1) {
         o << "    { VecT<" << T << ", " << V << "> w;\n      #pragma unroll\n      for (int j = 0; j < " << V
           << "; ++j) w.v[j] = " << st(n.dtype, "f" + std::to_string(op.first) + "[j]") << ";\n      *(VecT<" << T << ", "
           << V << ">*)((" << T << "*)" << P << " + chunk * " << V << "ull) = w; }\n";

@@ -381,6 +381,17 @@ int Planner::add_leaf(int rid, int slot, const View& v, DType dt) {
   L.slot = slot;
   L.view = v;
   L.dtype = dt;
+  if (P_.slots_[slot].kind == SlotKind::Const && !v.padded()) {
+    bool uniform = true;
+    for (size_t d = 0; d < v.shape.size(); ++d)
+      if (v.strides[d] != 0 && v.shape[d] > 1) uniform = false;
+    const Node& cn = g_.node(P_.slots_[slot].node);
+    size_t w = dt_width(dt);
+    if (uniform && cn.op.data && v.offset >= 0 && (size_t)(v.offset + 1) * w <= cn.op.data->size() && w <= 8) {
+      L.imm = true;
+      std::memcpy(L.imm_bits, cn.op.data->data() + (size_t)v.offset * w, w);
+    }
+  }
   R.leaves.push_back(L);
   depend(region_step_[rid], slot);
   RNode n;

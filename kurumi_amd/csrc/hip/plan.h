@@ -84,6 +84,10 @@ struct Leaf {
   int slot = -1;
   View view;          // over the region's iteration shape S (LINE leaves: stride 0 on the axis)
   DType dtype = DType::F32;
+  // a constant read at one element everywhere (all strides 0, unpadded): its stored bits,
+  // emitted as an immediate instead of a load
+  bool imm = false;
+  uint64_t imm_bits[2] = {0, 0};
 };
 
 struct Region {
