@@ -157,7 +157,7 @@ struct Gen {
   std::ostringstream o;
   int rank = 0, a = -1;
   bool flat = true;
-  int V = 1, TPL = 1, NC = 1, WG = 256, GPW = 1;
+  int V = 1, TPL = 1, NC = 1, WG = 256, GPW = 1, FK = 1;
   uint64_t lines = 1, L = 1, N = 1;
   bool idx64 = false;
   std::vector<int> param_slots;
@@ -245,6 +245,17 @@ struct Gen {
   // loads only in regions that also stream a full-size output (a reduce-only region, which
   // reads far more than it writes, measured slower with non-temporal loads).
   // KURUMI_HIP_NT overrides.
+  // Non-temporal accesses of flat (elementwise) kernels, bit 1 = stores, bit 2 = loads.
+  // Streaming stores are non-temporal by default (measured: copy 6.21 -> 6.35 TB/s, rope 67 ->
+  // 82 % of peak, SwiGLU gate 67 -> 80 %); non-temporal loads help a pure copy but slow the
+  // kernels that re-read an input through the cache (rope's halves). KURUMI_HIP_FLAT_NT overrides.
+  int flat_nt() const {
+    static const int v = [] {
+      const char* e = std::getenv("KURUMI_HIP_FLAT_NT");
+      return e ? std::atoi(e) : 1;
+    }();
+    return v;
+  }
   int nt_mode() const {
     static const int forced = [] {
       const char* e = std::getenv("KURUMI_HIP_NT");
@@ -425,6 +436,8 @@ void Gen::plan_layout() {
     TPL = 1;
     WG = 256;
     NC = 1;
+    const char* fk = std::getenv("KURUMI_HIP_FLAT_CPT");
+    FK = fk ? std::max(1, std::atoi(fk)) : 1;
     return;
   }
   uint64_t chunks = (L + V - 1) / V;
@@ -586,7 +599,7 @@ void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
   if (bf16_words(ni)) {
     // bf16 pairs stay packed in 32-bit words (the form the cache keeps); each value is its word's
     // low half shifted up or its high half masked
-    const bool ntl = !flat && (nt_mode() & 2);
+    const bool ntl = flat ? (flat_nt() & 2) != 0 : (nt_mode() & 2) != 0;
     o << "      u32 rw" << ni << "[" << V / 2 << "];\n";
     o << "      { VecT<u32, " << V / 2 << "> raw = " << (ntl ? "vld_nt(" : "*(") << "(const VecT<u32, " << V / 2
       << ">*)((const " << T << "*)" << P << " + (" << ix() << ")(" << base << " + (" << ix() << ")(" << c_expr
@@ -610,7 +623,7 @@ void Gen::emit_leaf_load(int ni, const std::string& c_expr) {
     o << "      } else {\n        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) r" << ni << "[j] = ("
       << T << ")0;\n      }\n";
   } else if (leaf_vec[n.leaf]) {
-    const bool ntl = !flat && (nt_mode() & 2);
+    const bool ntl = flat ? (flat_nt() & 2) != 0 : (nt_mode() & 2) != 0;
     o << "      { VecT<" << T << ", " << V << "> raw = " << (ntl ? "vld_nt(" : "*(") << "(const VecT<" << T << ", " << V
       << ">*)((const " << T << "*)" << P << " + (" << ix() << ")(" << base << " + (" << ix() << ")(" << c_expr
       << "))));\n";
@@ -915,9 +928,12 @@ std::string Gen::generate(RegionCode* rc) {
   int vecaxis = flat ? rank - 1 : a;
   std::vector<int> lines_leaves;
   if (flat) {
+    // FK chunks per thread, each a block-wide coalesced stripe, unrolled so their loads are in
+    // flight together
     uint64_t chunks = N / V;
-    o << "  const u64 chunk = (u64)blockIdx.x * " << WG << "ull + threadIdx.x;\n";
-    o << "  if (chunk >= " << chunks << "ull) return;\n";
+    o << "  #pragma unroll\n  for (int kk = 0; kk < " << FK << "; ++kk) {\n";
+    o << "  const u64 chunk = ((u64)blockIdx.x * " << FK << "ull + kk) * " << WG << "ull + threadIdx.x;\n";
+    o << "  if (chunk < " << chunks << "ull) {\n";
     o << "  const int lane = 0; (void)lane;\n";
     o << "  " << ix() << " t = (" << ix() << ")(chunk * " << V << "ull);\n";
     for (int d = rank - 1; d >= 0; --d) {
@@ -972,17 +988,19 @@ std::string Gen::generate(RegionCode* rc) {
         // every bf16 op result is already bf16-exact: pack pairs with one v_perm each
         o << "    { VecT<u32, " << V / 2 << "> w;\n      #pragma unroll\n      for (int jj = 0; jj < " << V / 2
           << "; ++jj) w.v[jj] = pack_bf16_exact(f" << op.first << "[2 * jj], f" << op.first << "[2 * jj + 1]);\n"
-          << "      *(VecT<u32, " << V / 2 << ">*)((" << T << "*)" << P << " + chunk * " << V << "ull) = w; }\n";
+          << "      " << (flat_nt() & 1 ? "vst_nt(" : "*(") << "(VecT<u32, " << V / 2 << ">*)((" << T << "*)" << P
+          << " + chunk * " << V << "ull)" << (flat_nt() & 1 ? ", w); }\n" : ") = w; }\n");
       } else if (V > 1) {
         o << "    { VecT<" << T << ", " << V << "> w;\n      #pragma unroll\n      for (int j = 0; j < " << V
-          << "; ++j) w.v[j] = " << st(n.dtype, "f" + std::to_string(op.first) + "[j]") << ";\n      *(VecT<" << T << ", "
-          << V << ">*)((" << T << "*)" << P << " + chunk * " << V << "ull) = w; }\n";
+          << "; ++j) w.v[j] = " << st(n.dtype, "f" + std::to_string(op.first) + "[j]") << ";\n      "
+          << (flat_nt() & 1 ? "vst_nt(" : "*(") << "(VecT<" << T << ", " << V << ">*)((" << T << "*)" << P << " + chunk * "
+          << V << "ull)" << (flat_nt() & 1 ? ", w); }\n" : ") = w; }\n");
       } else {
         o << "    ((" << T << "*)" << P << ")[chunk] = " << st(n.dtype, "f" + std::to_string(op.first) + "[0]") << ";\n";
       }
     }
-    o << "  }\n}\n";
-    rc->grid = (unsigned)((N / (uint64_t)V + WG - 1) / WG);
+    o << "  }\n  }\n  }\n}\n";
+    rc->grid = (unsigned)((N / (uint64_t)V + (uint64_t)WG * FK - 1) / ((uint64_t)WG * FK));
     rc->block = WG;
     rc->arg_slots = param_slots;
     return finish(prefix, rc);
