@@ -139,7 +139,9 @@ __global__ void __launch_bounds__(WM* WN * 64)
   __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[2 * (ABYTES + BBYTES)];
   KU_LDS unsigned char* lds = (KU_LDS unsigned char*)lds_raw;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, l32 = lane & 31;
+  // the wave index is uniform: kept in an SGPR, the DMA destinations (M0) need no VALU work
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5,
+            l32 = lane & 31;
   const int wm = wave / WN, wn = wave % WN;
   const int tm = (int)((a.m + BM - 1) / BM), tn = (int)((a.n + BN - 1) / BN);
   int im, in;
