@@ -7,7 +7,7 @@ single fused kernel's algorithmic traffic. Every config runs as a device-residen
 launches, then K timed launches bracketed by stream synchronisation. Per-kernel durations
 come from hipEvents recorded on the plan's own stream. The other configs are reported under
 "configs" with their own roofline fractions; config "6" is the nn primitives around them
-(rope, the SwiGLU gate, rmsnorm).
+(rope, the SwiGLU gate, rmsnorm, the int4 decode GEMV).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6] [--no-cpu]
 """
@@ -297,6 +297,33 @@ def bench_nn(hip, steps, warmup):
     return out
 
 
+def bench_quant(hip, steps, warmup):
+    """Weight-only int4 decode GEMV (QuantMatmul, M = 1): one token through a [11008, 4096] int4
+    projection (symmetric, group 128, bf16 activations) per layer, 12 layers' weights per plan
+    (12 x 23 MB exceeds the 256 MB last-level cache). HBM-bound on the packed weights + scales."""
+    K = _ku()
+    n, k, grp, layers = 11008, 4096, 128, 12
+    rng = np.random.default_rng(0)
+    g = K.Graph()
+    x = g.input([1, k], K.DType.BF16)
+    roots = []
+    for li in range(layers):
+        w = rng.standard_normal((n, k), dtype=np.float32)
+        packed, scales, _ = K.quantize(w, 4, grp, True)
+        qw = g.constant_bytes(K.DType.U8, packed.tobytes(), packed.shape)
+        sc = g.constant_bytes(K.DType.F16, scales.tobytes(), scales.shape)
+        roots.append(g.quant_matmul(x, qw, sc, None, 4, grp))
+    xt = device_values(hip, scaled_randn(1.0), [1, k], 601, K.DType.BF16)
+    plan = hip.plan(g, roots, {x: xt})
+    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    kms = sum(per_step) / layers
+    algo = n * k // 2 + n * (k // grp) * 2 + k * 2 + n * 2  # packed weight, scales, act, out
+    return {"nn_quant_gemv": {"workload": f"int4 (sym, group {grp}) decode GEMV [1,{k}] x [{n},{k}]^T bf16, "
+                              f"{layers} layers' weights per plan", "ms_per_step": wall_ms / layers,
+                              "kernels": labels[:1], "kernel_ms": per_step[:1], "algo_bytes": algo,
+                              "roofline": roofline_hbm(algo, kms)}}
+
+
 def bench_copy(hip, steps, warmup):
     """A plain streaming copy of 2^28 f32 (1 GiB read + 1 GiB write) through a one-leaf region."""
     K = _ku()
@@ -355,6 +382,7 @@ def main() -> int:
         extra["cfg5"] = bench_fp8(hip, max(3, args.steps // 4), 1)
     if "6" in cfgs:
         extra.update(bench_nn(hip, args.steps, args.warmup))
+        extra.update(bench_quant(hip, args.steps, args.warmup))
     if args.probe_copy:
         extra["copy_probe"] = bench_copy(hip, args.steps, args.warmup)
     cpu = None if args.no_cpu else cpu_baseline_cfg2(xt)

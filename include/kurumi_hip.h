@@ -113,6 +113,13 @@ KuNode ku_matmul(KuGraph *g, KuNode a, KuNode b);
 KuNode ku_dot_general(KuGraph *g, KuNode a, KuNode b, const size_t *lc, size_t nlc, const size_t *rc, size_t nrc,
                       const size_t *lb, size_t nlb, const size_t *rb, size_t nrb);
 
+/* weight-only quantized matmul: act[M,K] x dequant(qweight)[N,K]^T -> [M,N] (kurumi.h:225-234);
+ * qweight KU_U8-packed, scales/mins KU_F16 [N, K/group_size], mins = KU_ERR for symmetric */
+KuNode ku_quant_matmul(KuGraph *g, KuNode act, KuNode qweight, KuNode scales, KuNode mins, uint8_t bits,
+                       size_t group_size);
+void ku_quantize(const float *w, size_t rows, size_t cols, uint8_t bits, size_t group_size, uint32_t symmetric,
+                 uint8_t *out_packed, uint16_t *out_scales, uint16_t *out_mins);
+
 /* movement: kurumi.h:269-276, 286-292 */
 KuNode ku_reshape(KuGraph *g, KuNode x, const size_t *shape, size_t rank);
 KuNode ku_expand(KuGraph *g, KuNode x, const size_t *shape, size_t rank);

@@ -147,6 +147,9 @@ def _declare(L: C.CDLL) -> None:
         "ku_hip_plan_free": ([P], None),
         "ku_hip_codegen": ([P, C.POINTER(C.c_uint32), sz, u32, C.c_char_p, sz], sz),
         "ku_hip_profile": ([P, C.POINTER(C.c_uint64), sz], C.c_uint64),
+        "ku_quant_matmul": ([P, u32, u32, u32, u32, C.c_uint8, sz], u32),
+        "ku_quantize": ([C.POINTER(C.c_float), sz, sz, C.c_uint8, sz, u32, C.c_char_p, C.POINTER(C.c_uint16),
+                         C.POINTER(C.c_uint16)], None),
         "ku_graph_serialize": ([P, C.POINTER(u32), sz, C.POINTER(u32), C.POINTER(C.c_uint8),
                                 C.POINTER(C.c_char_p), sz, C.c_char_p, sz], sz),
         "ku_graph_serialize_reachable": ([P, C.POINTER(u32), sz, C.POINTER(u32), C.POINTER(C.c_uint8),
@@ -316,6 +319,10 @@ class Graph:
             arr, n = _shape(v)
             args += [arr, n]
         return self._n("ku_dot_general", a, b, *args)
+
+    def quant_matmul(self, act: int, qweight: int, scales: int, mins: int | None, bits: int, group_size: int) -> int:
+        """act [M, K] x dequant(qweight)[N, K]^T (graph/ops/core/contract.rs:49-115); mins None = symmetric."""
+        return self._n("ku_quant_matmul", act, qweight, scales, KU_ERR if mins is None else mins, bits, group_size)
 
     def reshape(self, x: int, shape: Sequence[int]) -> int:
         s, r = _shape(shape)
@@ -580,6 +587,22 @@ def deserialize_multi(blob: bytes) -> Runnable:
 def deserialize_graph(blob: bytes) -> Runnable:
     """Same as ``deserialize_multi``; ``outputs``/``inputs`` read entry 0 (decode.rs:20-24)."""
     return deserialize_multi(blob)
+
+
+def quantize(w: np.ndarray, bits: int, group_size: int, symmetric: bool):
+    """ku_quantize (kurumi_core/src/quant.rs:43-91): f32 [rows, cols] -> (packed u8 [rows, cols*bits/8],
+    scales f16 bits u16 [rows, cols/group], mins u16 or None)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, cols = w.shape
+    if bits not in (2, 4, 8) or group_size <= 0 or cols % group_size or cols * bits % 8:
+        raise KuError("quantize: bits must be 2, 4 or 8 and group_size must divide cols")
+    packed = np.zeros((rows, cols * bits // 8), np.uint8)
+    scales = np.zeros((rows, cols // group_size), np.uint16)
+    mins = None if symmetric else np.zeros((rows, cols // group_size), np.uint16)
+    lib().ku_quantize(w.ctypes.data_as(C.POINTER(C.c_float)), rows, cols, bits, group_size, int(symmetric),
+                      packed.ctypes.data_as(C.c_char_p), scales.ctypes.data_as(C.POINTER(C.c_uint16)),
+                      None if mins is None else mins.ctypes.data_as(C.POINTER(C.c_uint16)))
+    return packed, scales, mins
 
 
 def amp_fp8(g: Graph, root: int) -> int:

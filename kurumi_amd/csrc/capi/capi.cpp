@@ -14,6 +14,7 @@
 #include "errors.h"
 #include "handles.h"
 #include "../ir/graph.h"
+#include "../ir/quant.h"
 #include "../ir/tensor.h"
 
 using ku::NodeId;
@@ -180,6 +181,30 @@ KuNode ku_dot_general(KuGraph* g, KuNode a, KuNode b, const size_t* lc, size_t n
                       const size_t* lb, size_t nlb, const size_t* rb, size_t nrb) {
   return build(g, "ku_dot_general", [&](ku::Graph& gr) {
     return gr.dot_general(a, b, mk_shape(lc, nlc), mk_shape(rc, nrc), mk_shape(lb, nlb), mk_shape(rb, nrb));
+  });
+}
+
+// capi/ops/contract.rs:42-54: mins = KU_ERR selects the symmetric form
+KuNode ku_quant_matmul(KuGraph* g, KuNode act, KuNode qweight, KuNode scales, KuNode mins, uint8_t bits,
+                       size_t group_size) {
+  return build(g, "ku_quant_matmul", [&](ku::Graph& gr) {
+    return gr.quant_matmul(act, qweight, scales, mins == KU_ERR ? ku::Graph::kNoNode : mins, bits, group_size);
+  });
+}
+
+// capi/ops/contract.rs:56-84
+void ku_quantize(const float* w, size_t rows, size_t cols, uint8_t bits, size_t group_size, uint32_t symmetric,
+                 uint8_t* out_packed, uint16_t* out_scales, uint16_t* out_mins) {
+  if (!w || !out_packed || !out_scales) {
+    set_err("ku_quantize: null w/out_packed/out_scales");
+    return;
+  }
+  guard<int>(0, [&] {
+    ku::Quantized q = ku::quantize(w, rows, cols, bits, group_size, symmetric != 0);
+    std::memcpy(out_packed, q.packed.data(), q.packed.size());
+    std::memcpy(out_scales, q.scales.data(), q.scales.size() * 2);
+    if (!q.mins.empty() && out_mins) std::memcpy(out_mins, q.mins.data(), q.mins.size() * 2);
+    return 0;
   });
 }
 

@@ -43,4 +43,22 @@ const char* attn_variant(const AttnArgs& a);
 bool attn_supported(const AttnArgs& a);
 void launch_attention(const AttnArgs& a, hipStream_t s);
 
+// Weight-only quantized matmul (quant.hip): out[M, N] = act[M, K] x dequant(qw)[N, K]^T.
+struct QuantArgs {
+  const void* act = nullptr;          // [M, K] contiguous, act_type
+  const uint8_t* qw = nullptr;        // [N, K * bits / 8] packed, low field first
+  const uint16_t* scales = nullptr;   // f16 [N, K / group]
+  const uint16_t* mins = nullptr;     // f16 [N, K / group], asymmetric only
+  void* out = nullptr;                // [M, N] contiguous, act_type
+  void* wdq = nullptr;                // dequantized weight [N, K] (wdq_type) for the GEMM path
+  int64_t m = 0, n = 0, k = 0, group = 0;
+  int bits = 4;
+  bool sym = true;
+  int act_type = GT_BF16;
+  int wdq_type = GT_BF16;
+};
+bool quant_gemv_ok(const QuantArgs& a);
+void launch_quant_gemv(const QuantArgs& a, hipStream_t s);
+void launch_quant_dequant(const QuantArgs& a, hipStream_t s);
+
 }  // namespace ku::hipbk

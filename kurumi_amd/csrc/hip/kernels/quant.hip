@@ -1,0 +1,294 @@
+// Weight-only quantized matmul for gfx950 (kernel family 5):
+// out[m][n] = sum_k act[m][k] * dequant(qweight)[n][k], the semantics of `Op::QuantMatmul`
+// (kurumi_core/src/interp/contract.rs:69-99 over quant.rs:100-133): 2/4/8-bit fields packed
+// row-major along K, low field first; one f16 scale per group of `group` K columns, plus an f16
+// min when asymmetric (w = q * s + min) or a sign-extended field when symmetric (w = q * s);
+// f32 products and accumulation, the result rounded once to act's dtype.
+//
+// quant_gemv_k (M <= 4, the decode shapes): the weight is read from HBM exactly once and
+// dequantized in registers; eight weight rows per work-group share each act value a thread
+// loads, and their 16-byte chunks are all in flight at once.
+// quant_dequant_k (M > 4): the weight is expanded once into act's dtype (f32, bf16 or f16) for
+// the MFMA / generic GEMM; bf16 / f16 round each dequantized weight once, the f32 products then
+// accumulate in f32 like the reference.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "kernels.h"
+#include "numeric.h"
+
+namespace ku::hipbk {
+
+namespace {
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int GEMV_RW = 8;  // weight rows per work-group
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+template <int AT>
+__device__ __forceinline__ float act_ld(const void* p, int64_t i) {
+  if constexpr (AT == GT_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (AT == GT_BF16) return __uint_as_float((uint32_t) static_cast<const uint16_t*>(p)[i] << 16);
+  else return f16_to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+
+template <int AT>
+__device__ __forceinline__ void act_st(void* p, int64_t i, float v) {
+  if constexpr (AT == GT_F32) static_cast<float*>(p)[i] = v;
+  else if constexpr (AT == GT_BF16) static_cast<uint16_t*>(p)[i] = d_bf16_st(v);
+  else static_cast<uint16_t*>(p)[i] = d_f16_st(v);
+}
+
+// field i (0 .. 8/BITS - 1 per byte) of packed byte b, dequantized with scale s / min mn; the
+// product is not fused with the min (the reference rounds q * s, then adds)
+template <int BITS, bool SYM>
+__device__ __forceinline__ float deq(uint32_t raw, float s, float mn) {
+  if constexpr (SYM) {
+    const int v = (int)(raw << (32 - BITS)) >> (32 - BITS);
+    return __fmul_rn((float)v, s);
+  } else {
+    return __fadd_rn(__fmul_rn((float)raw, s), mn);
+  }
+}
+
+__device__ __forceinline__ float wave_add(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+// V consecutive act values of one row as f32 (one or two 16-byte loads when V allows)
+template <int AT, int V>
+__device__ __forceinline__ void load_act(const void* act, int64_t idx, float (&av)[V]) {
+  if constexpr (AT == GT_F32 && V % 4 == 0) {
+    const float* p = static_cast<const float*>(act) + idx;
+#pragma unroll
+    for (int q = 0; q < V / 4; ++q) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(p + 4 * q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[4 * q + i] = __uint_as_float(v[i]);
+    }
+  } else if constexpr (AT != GT_F32 && V % 8 == 0) {
+    const uint16_t* p = static_cast<const uint16_t*>(act) + idx;
+#pragma unroll
+    for (int q = 0; q < V / 8; ++q) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(p + 8 * q);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint16_t h = (uint16_t)(v[i >> 1] >> ((i & 1) * 16));
+        av[8 * q + i] = AT == GT_BF16 ? __uint_as_float((uint32_t)h << 16) : f16_to_f32(h);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < V; ++i) av[i] = act_ld<AT>(act, idx + i);
+  }
+}
+
+// A work-group takes GEMV_RW weight rows; its threads stride over the K chunks of CB packed
+// bytes (E values). Per chunk a thread issues the loads of all GEMV_RW rows first (they are in
+// flight together), then walks the chunk V values at a time: each act value is loaded once for
+// all weight rows. OG: a chunk lies inside one scale group (one scale / min per row and chunk);
+// otherwise each value looks its group up. Partial dots are folded by a wave reduction and an
+// LDS sum across waves.
+template <int BITS, bool SYM, int AT, int MB, int CB, bool OG>
+__global__ void __launch_bounds__(256) quant_gemv_k(QuantArgs a) {
+  constexpr int PER = 8 / BITS, E = CB * PER;  // weight values per thread and chunk
+  constexpr int V = E < 8 ? E : 8;             // act values loaded at a time
+  __shared__ float red[4][GEMV_RW * MB];
+  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6, nwv = nt >> 6;
+  const int64_t K = a.k, N = a.n, rb = K * BITS / 8, ng = K / a.group, nch = K / E;
+  const int64_t row0 = (int64_t)blockIdx.x * GEMV_RW;
+  int64_t rows[GEMV_RW];
+#pragma unroll
+  for (int r = 0; r < GEMV_RW; ++r) rows[r] = row0 + r < N ? row0 + r : N - 1;  // duplicates never stored
+  float acc[GEMV_RW][MB];
+#pragma unroll
+  for (int r = 0; r < GEMV_RW; ++r)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[r][m] = 0.f;
+  for (int64_t c = tid; c < nch; c += nt) {
+    const int64_t k = c * E;
+    uint32_t wb[GEMV_RW][(CB + 3) / 4];
+#pragma unroll
+    for (int r = 0; r < GEMV_RW; ++r) {
+      const uint8_t* p = a.qw + rows[r] * rb + k / PER;
+      if constexpr (CB == 16) {
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wb[r][j] = w[j];
+      } else if constexpr (CB == 8) {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        wb[r][0] = w[0];
+        wb[r][1] = w[1];
+      } else {
+        wb[r][0] = p[0];
+      }
+    }
+    float s[GEMV_RW], mn[GEMV_RW];
+    if constexpr (OG) {
+#pragma unroll
+      for (int r = 0; r < GEMV_RW; ++r) {
+        const int64_t gi = rows[r] * ng + k / a.group;
+        s[r] = f16_to_f32(a.scales[gi]);
+        mn[r] = SYM ? 0.f : f16_to_f32(a.mins[gi]);
+      }
+    }
+#pragma unroll
+    for (int e0 = 0; e0 < E; e0 += V) {
+      float av[MB][V];
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        if (m < a.m) load_act<AT, V>(a.act, m * K + k + e0, av[m]);
+        else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) av[m][e] = 0.f;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < GEMV_RW; ++r)
+#pragma unroll
+        for (int e = 0; e < V; ++e) {
+          const int ei = e0 + e;
+          if constexpr (!OG) {
+            const int64_t gi = rows[r] * ng + (k + ei) / a.group;
+            s[r] = f16_to_f32(a.scales[gi]);
+            mn[r] = SYM ? 0.f : f16_to_f32(a.mins[gi]);
+          }
+          const uint32_t raw = (wb[r][ei / (4 * PER)] >> ((ei % (4 * PER)) * BITS)) & ((1u << BITS) - 1);
+          const float w = deq<BITS, SYM>(raw, s[r], mn[r]);
+#pragma unroll
+          for (int m = 0; m < MB; ++m) acc[r][m] = fmaf(av[m][e], w, acc[r][m]);
+        }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < GEMV_RW; ++r)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const float v = wave_add(acc[r][m]);
+      if (lane == 0) red[wave][r * MB + m] = v;
+    }
+  __syncthreads();
+  if (tid < GEMV_RW * MB) {
+    const int r = tid / MB, m = tid % MB;
+    float v = red[0][tid];
+    for (int w = 1; w < nwv; ++w) v += red[w][tid];
+    const int64_t n = row0 + r;
+    if (n < N && m < a.m) act_st<AT>(a.out, m * N + n, v);
+  }
+}
+
+// one thread per packed byte of the weight: its 8/BITS values into wdq [N, K] (dtype WT)
+template <int BITS, bool SYM, int WT>
+__global__ void __launch_bounds__(256) quant_dequant_k(QuantArgs a) {
+  constexpr int PER = 8 / BITS;
+  const int64_t rb = a.k * BITS / 8, ng = a.k / a.group;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= a.n * rb) return;
+  const int64_t n = i / rb, k0 = (i % rb) * PER;
+  const uint32_t b = a.qw[i];
+#pragma unroll
+  for (int f = 0; f < PER; ++f) {
+    const int64_t gi = n * ng + (k0 + f) / a.group;
+    const float s = f16_to_f32(a.scales[gi]);
+    const float mn = SYM ? 0.f : f16_to_f32(a.mins[gi]);
+    act_st<WT>(a.wdq, n * a.k + k0 + f, deq<BITS, SYM>((b >> (f * BITS)) & ((1u << BITS) - 1), s, mn));
+  }
+}
+
+template <int BITS, bool SYM, int AT, int MB>
+void gemv_mb(const QuantArgs& a, hipStream_t s) {
+  // 16 packed bytes per thread and chunk (8 for int2: E = 32 values either way) when rows are
+  // whole chunks and groups whole chunks; otherwise single bytes (one group per byte when the
+  // group is a multiple of the fields per byte, else a group lookup per value)
+  constexpr int CB = BITS == 2 ? 8 : 16, PER = 8 / BITS;
+  const int64_t rb = a.k * BITS / 8;
+  const int kind = (rb % CB == 0 && a.group % (CB * PER) == 0) ? 0 : (a.group % PER == 0 ? 1 : 2);
+  const int64_t nch = kind == 0 ? rb / CB : rb;
+  const int nwv = (int)std::min<int64_t>(4, std::max<int64_t>(1, (nch + 63) / 64));
+  const dim3 grid((unsigned)((a.n + GEMV_RW - 1) / GEMV_RW)), block((unsigned)(nwv * 64));
+  if (kind == 0) hipLaunchKernelGGL((quant_gemv_k<BITS, SYM, AT, MB, CB, true>), grid, block, 0, s, a);
+  else if (kind == 1) hipLaunchKernelGGL((quant_gemv_k<BITS, SYM, AT, MB, 1, true>), grid, block, 0, s, a);
+  else hipLaunchKernelGGL((quant_gemv_k<BITS, SYM, AT, MB, 1, false>), grid, block, 0, s, a);
+}
+
+template <int BITS, bool SYM, int AT>
+void gemv_at(const QuantArgs& a, hipStream_t s) {
+  switch (a.m) {
+    case 1: gemv_mb<BITS, SYM, AT, 1>(a, s); return;
+    case 2: gemv_mb<BITS, SYM, AT, 2>(a, s); return;
+    default: gemv_mb<BITS, SYM, AT, 4>(a, s); return;
+  }
+}
+
+template <int BITS, bool SYM>
+void gemv_bits(const QuantArgs& a, hipStream_t s) {
+  switch (a.act_type) {
+    case GT_F32: gemv_at<BITS, SYM, GT_F32>(a, s); return;
+    case GT_BF16: gemv_at<BITS, SYM, GT_BF16>(a, s); return;
+    default: gemv_at<BITS, SYM, GT_F16>(a, s); return;
+  }
+}
+
+template <int BITS, bool SYM>
+void dequant_bits(const QuantArgs& a, hipStream_t s) {
+  const int64_t total = a.n * (a.k * BITS / 8);
+  const dim3 grid((unsigned)((total + 255) / 256));
+  switch (a.wdq_type) {
+    case GT_F32: hipLaunchKernelGGL((quant_dequant_k<BITS, SYM, GT_F32>), grid, dim3(256), 0, s, a); return;
+    case GT_BF16: hipLaunchKernelGGL((quant_dequant_k<BITS, SYM, GT_BF16>), grid, dim3(256), 0, s, a); return;
+    default: hipLaunchKernelGGL((quant_dequant_k<BITS, SYM, GT_F16>), grid, dim3(256), 0, s, a); return;
+  }
+}
+
+void check(const QuantArgs& a) {
+  if (!(a.bits == 2 || a.bits == 4 || a.bits == 8)) throw std::runtime_error("quant: bits must be 2, 4 or 8");
+  if (a.group <= 0 || a.k % a.group) throw std::runtime_error("quant: group must divide K");
+  if (!(a.act_type == GT_F32 || a.act_type == GT_BF16 || a.act_type == GT_F16))
+    throw std::runtime_error("quant: act must be f32, bf16 or f16");
+  if (a.k * a.bits % 8) throw std::runtime_error("quant: K * bits must be whole bytes");
+  if (!a.sym && !a.mins) throw std::runtime_error("quant: asymmetric weights need mins");
+}
+
+}  // namespace
+
+bool quant_gemv_ok(const QuantArgs& a) { return a.m >= 1 && a.m <= 4; }
+
+void launch_quant_gemv(const QuantArgs& a, hipStream_t s) {
+  check(a);
+  if (!quant_gemv_ok(a)) throw std::runtime_error("quant: the GEMV kernel takes M <= 4");
+  if (a.n == 0) return;
+  if (reinterpret_cast<uintptr_t>(a.qw) & 15)
+    throw std::runtime_error("quant: packed weight must be 16-byte aligned");
+  switch (a.bits * 2 + (a.sym ? 1 : 0)) {
+    case 5: gemv_bits<2, true>(a, s); return;
+    case 4: gemv_bits<2, false>(a, s); return;
+    case 9: gemv_bits<4, true>(a, s); return;
+    case 8: gemv_bits<4, false>(a, s); return;
+    case 17: gemv_bits<8, true>(a, s); return;
+    default: gemv_bits<8, false>(a, s); return;
+  }
+}
+
+void launch_quant_dequant(const QuantArgs& a, hipStream_t s) {
+  check(a);
+  if (a.n == 0 || a.k == 0) return;
+  switch (a.bits * 2 + (a.sym ? 1 : 0)) {
+    case 5: dequant_bits<2, true>(a, s); return;
+    case 4: dequant_bits<2, false>(a, s); return;
+    case 9: dequant_bits<4, true>(a, s); return;
+    case 8: dequant_bits<4, false>(a, s); return;
+    case 17: dequant_bits<8, true>(a, s); return;
+    default: dequant_bits<8, false>(a, s); return;
+  }
+}
+
+}  // namespace ku::hipbk

@@ -345,6 +345,7 @@ class Planner {
   void visit_rowop(NodeId id);
   void visit_dot(NodeId id);
   void visit_sdpa(NodeId id);
+  void visit_quant(NodeId id);
   int copy_view_to_slot(const View& v, int slot_src, DType dt, NodeId node);
 
   // pattern pre-pass
@@ -1023,6 +1024,47 @@ void Planner::visit_dot(NodeId id) {
   if (target != id) vals_[target].view = View::contiguous(g_.shape(target));
 }
 
+// Op::QuantMatmul (graph/ops/core/contract.rs:49-115): every operand as a contiguous device
+// buffer; the output [M, N] in act's dtype.
+void Planner::visit_quant(NodeId id) {
+  const Node& n = g_.node(id);
+  QuantStep Q;
+  const DType at = g_.dtype(n.src[0]);
+  if (!(at == DType::F32 || at == DType::BF16 || at == DType::F16))
+    throw Error(std::string("kurumi_hip: quant_matmul act dtype ") + dt_name(at) + " is not supported on device");
+  int slots[4] = {-1, -1, -1, -1};
+  int64_t offs[4] = {0, 0, 0, 0};
+  for (size_t i = 0; i < n.src.size(); ++i) {
+    View v = dev_view_of(n.src[i]);
+    slots[i] = vals_[n.src[i]].slot;
+    if (!v.is_contiguous()) {  // the kernels take dense, 16-byte-aligned operands
+      slots[i] = copy_view_to_slot(v, slots[i], g_.dtype(n.src[i]), n.src[i]);
+      v = View::contiguous(v.shape);
+    }
+    offs[i] = v.offset;
+  }
+  const Shape& as = g_.shape(n.src[0]);
+  Q.act_slot = slots[0]; Q.qw_slot = slots[1]; Q.sc_slot = slots[2]; Q.mn_slot = slots[3];
+  Q.act_off = offs[0]; Q.qw_off = offs[1]; Q.sc_off = offs[2]; Q.mn_off = offs[3];
+  Q.m = as[0]; Q.k = as[1]; Q.n = n.shape[1];
+  Q.group = n.op.qgroup; Q.bits = n.op.qbits; Q.sym = n.op.qsym;
+  Q.act_dtype = at;
+  Q.wdq_dtype = at;  // bf16 / f16 act: the MFMA GEMM on rounded weights; f32: the generic GEMM
+  Q.out_slot = new_slot(SlotKind::Temp, at, Q.m * Q.n * dt_width(at), id);
+  if (!(Q.m >= 1 && Q.m <= 4)) Q.wdq_slot = new_slot(SlotKind::Temp, Q.wdq_dtype, Q.n * Q.k * dt_width(Q.wdq_dtype), id);
+  P_.quants_.push_back(Q);
+  int step = new_step(Step::QUANT, (int)P_.quants_.size() - 1, "quant");
+  for (int i = 0; i < 4; ++i)
+    if (slots[i] >= 0) depend(step, slots[i]);
+  slot_producer_[Q.out_slot] = step;
+  if (Q.wdq_slot >= 0) slot_producer_[Q.wdq_slot] = step;
+  Val v;
+  v.k = Val::Dev;
+  v.slot = Q.out_slot;
+  v.view = View::contiguous(n.shape);
+  vals_[id] = v;
+}
+
 void Planner::visit_sdpa(NodeId id) {
   const Node& n = g_.node(id);
   AttnPattern pat;
@@ -1325,6 +1367,9 @@ void Planner::visit(NodeId id) {
     case OpKind::Sdpa:
       visit_sdpa(id);
       return;
+    case OpKind::QuantMatmul:
+      visit_quant(id);
+      return;
     default:
       if (is_elementwise(n.op.kind)) {
         if (dt_is_complex(n.dtype) || (n.src.size() && dt_is_complex(g_.dtype(n.src[0]))))
@@ -1435,6 +1480,12 @@ void Plan::compile() {
       std::ostringstream o;
       o << gemm_variant(a) << " b" << G.batch << " m" << G.m << " n" << G.n << " k" << G.k;
       s.label = o.str();
+    } else if (s.type == Step::QUANT) {
+      const QuantStep& Q = quants_[s.index];
+      std::ostringstream o;
+      o << (Q.wdq_slot < 0 ? "quant_gemv" : "quant_dequant+gemm") << " int" << Q.bits << (Q.sym ? "s" : "a") << " g"
+        << Q.group << " m" << Q.m << " n" << Q.n << " k" << Q.k;
+      s.label = o.str();
     } else {
       const AttnStep& A = attns_[s.index];
       AttnArgs a;
@@ -1517,6 +1568,34 @@ void Plan::launch_step(const Step& s) {
                    (long long)a.sbk, (long long)a.sbn, (long long)a.batch, (long long)a.m, (long long)a.n,
                    (long long)a.k, a.in_type, a.out_type);
     launch_gemm(a, st);
+    KU_HIP(hipGetLastError());
+    ctx_->profile().launches[(int)Kind::Gemm]++;
+  } else if (s.type == Step::QUANT) {
+    const QuantStep& Q = quants_[s.index];
+    QuantArgs a;
+    a.act = static_cast<const char*>(slot_ptr(slots_, Q.act_slot)) + Q.act_off * (int64_t)dt_width(Q.act_dtype);
+    a.qw = static_cast<const uint8_t*>(slot_ptr(slots_, Q.qw_slot)) + Q.qw_off;
+    a.scales = static_cast<const uint16_t*>(slot_ptr(slots_, Q.sc_slot)) + Q.sc_off;
+    if (Q.mn_slot >= 0) a.mins = static_cast<const uint16_t*>(slot_ptr(slots_, Q.mn_slot)) + Q.mn_off;
+    a.out = slot_ptr(slots_, Q.out_slot);
+    a.m = (int64_t)Q.m; a.n = (int64_t)Q.n; a.k = (int64_t)Q.k; a.group = (int64_t)Q.group;
+    a.bits = Q.bits; a.sym = Q.sym;
+    a.act_type = (int)Q.act_dtype; a.wdq_type = (int)Q.wdq_dtype;
+    if (Q.m * Q.n == 0) return;
+    if (Q.wdq_slot < 0) {
+      launch_quant_gemv(a, st);
+    } else {
+      a.wdq = slot_ptr(slots_, Q.wdq_slot);
+      launch_quant_dequant(a, st);
+      KU_HIP(hipGetLastError());
+      GemmArgs g;
+      g.a = a.act; g.b = a.wdq; g.c = a.out;
+      g.sam = (int64_t)Q.k; g.sak = 1; g.sab = 0;
+      g.sbn = (int64_t)Q.k; g.sbk = 1; g.sbb = 0;  // B[k][n] = wdq[n][k]: the NT layout
+      g.batch = 1; g.m = a.m; g.n = a.n; g.k = a.k;
+      g.in_type = (int)Q.wdq_dtype; g.out_type = (int)Q.act_dtype;
+      launch_gemm(g, st);
+    }
     KU_HIP(hipGetLastError());
     ctx_->profile().launches[(int)Kind::Gemm]++;
   } else {

@@ -114,6 +114,17 @@ struct GemmStep {
   std::string variant;
 };
 
+// Weight-only quantized matmul: a fused dequant GEMV (M <= 4), else a dequantize pass into
+// `wdq_slot` followed by a GEMM of act x wdq^T.
+struct QuantStep {
+  int act_slot = -1, qw_slot = -1, sc_slot = -1, mn_slot = -1, out_slot = -1, wdq_slot = -1;
+  int64_t act_off = 0, qw_off = 0, sc_off = 0, mn_off = 0;  // elements
+  size_t m = 0, n = 0, k = 0, group = 0;
+  int bits = 4;
+  bool sym = true;
+  DType act_dtype = DType::BF16, wdq_dtype = DType::BF16;
+};
+
 struct AttnStep {
   int q_slot = -1, k_slot = -1, v_slot = -1, o_slot = -1;
   size_t bh = 0, s = 0, d = 0;
@@ -123,7 +134,7 @@ struct AttnStep {
 };
 
 struct Step {
-  enum Type { REGION, GEMM, ATTN } type;
+  enum Type { REGION, GEMM, ATTN, QUANT } type;
   int index;             // into regions / gemms / attns
   std::set<int> deps;    // producer step ids
   // compiled launch (regions)
@@ -173,6 +184,7 @@ class Plan {
   std::vector<Region> regions_;
   std::vector<GemmStep> gemms_;
   std::vector<AttnStep> attns_;
+  std::vector<QuantStep> quants_;
   std::vector<Step> steps_;
   std::vector<int> order_;                 // execution order of steps
   std::map<NodeId, int> input_slots_;

@@ -16,7 +16,8 @@ const char* op_name(OpKind k) {
                             "Add", "Mul", "Max", "Neg", "IDiv", "And", "Or", "Xor", "Shl", "Shr",
                             "CmpLt", "CmpEq", "Where", "Recip", "Sqrt", "Exp2", "Log2", "Sin", "Floor",
                             "Sum", "Prod", "ReduceMax", "ArgReduce", "Softmax", "RmsNorm", "Sdpa",
-                            "Reshape", "Permute", "Expand", "Slice", "Flip", "Pad", "DotGeneral"};
+                            "Reshape", "Permute", "Expand", "Slice", "Flip", "Pad", "DotGeneral",
+                            "QuantMatmul"};
   uint32_t i = static_cast<uint32_t>(k);
   return i < static_cast<uint32_t>(OpKind::NumKinds) ? n[i] : "?";
 }
@@ -119,6 +120,7 @@ Shape Graph::derive_shape(const Op& op, const std::vector<NodeId>& src) const {
       for (size_t i : free_axes(b.size(), op.rb, op.rc)) s.push_back(b[i]);
       return s;
     }
+    case OpKind::QuantMatmul: return {is(0)[0], is(1)[0]};  // infer.rs:132
     default: return is(0);  // elementwise, Softmax, RmsNorm, Sdpa, Flip
   }
 }
@@ -742,6 +744,44 @@ NodeId Graph::dot_general(NodeId a, NodeId b, const std::vector<size_t>& lc, con
   return push(std::move(op), {a, b});
 }
 
+// graph/ops/core/contract.rs:49-115: the reference's record-time checks, in its order.
+NodeId Graph::quant_matmul(NodeId act, NodeId qw, NodeId scales, NodeId mins, int bits, size_t group_size) {
+  const char* nm = "quant_matmul";
+  check_id(nm, act); check_id(nm, qw); check_id(nm, scales);
+  if (mins != kNoNode) check_id(nm, mins);
+  const Shape &sa = shape(act), &sq = shape(qw);
+  if (sa.size() != 2 || sq.size() != 2)
+    throw Error(std::string(nm) + ": act rank " + std::to_string(sa.size()) + ", qweight rank " +
+                std::to_string(sq.size()) + ": both must be rank-2");
+  if (dtype(qw) != DType::U8) throw Error(std::string(nm) + ": qweight must be U8, got " + dt_name(dtype(qw)));
+  if (dtype(scales) != DType::F16) throw Error(std::string(nm) + ": scales must be F16, got " + dt_name(dtype(scales)));
+  if (mins != kNoNode && dtype(mins) != DType::F16)
+    throw Error(std::string(nm) + ": mins must be F16, got " + dt_name(dtype(mins)));
+  if (!dt_is_float(dtype(act))) throw Error(std::string(nm) + ": act must be float, got " + dt_name(dtype(act)));
+  const size_t k = sa[1], n = sq[0];
+  if (!(bits == 2 || bits == 4 || bits == 8))
+    throw Error(std::string(nm) + ": bits " + std::to_string(bits) + " must be 2, 4, or 8");
+  if (group_size == 0 || k % group_size != 0)
+    throw Error(std::string(nm) + ": K " + std::to_string(k) + " must be a nonzero multiple of group_size " +
+                std::to_string(group_size));
+  if (sq[1] * 8 != k * (size_t)bits)
+    throw Error(std::string(nm) + ": qweight cols " + std::to_string(sq[1]) + " must equal K*bits/8 = " +
+                std::to_string(k) + "*" + std::to_string(bits) + "/8");
+  const size_t want = n * (k / group_size);
+  if (numel(shape(scales)) != want)
+    throw Error(std::string(nm) + ": scales must have N*K/group_size = " + std::to_string(want) + " entries");
+  if (mins != kNoNode && numel(shape(mins)) != want)
+    throw Error(std::string(nm) + ": mins must have N*K/group_size = " + std::to_string(want) + " entries");
+  Op op;
+  op.kind = OpKind::QuantMatmul;
+  op.qbits = bits;
+  op.qgroup = group_size;
+  op.qsym = mins == kNoNode;
+  std::vector<NodeId> src = {act, qw, scales};
+  if (mins != kNoNode) src.push_back(mins);
+  return push(std::move(op), std::move(src));
+}
+
 // capi/ops/contract.rs:11-13: ku_matmul = 2D dot_general contracting a's axis 1 with b's axis 0.
 NodeId Graph::matmul(NodeId a, NodeId b) {
   check_id("matmul", a); check_id("matmul", b);
@@ -784,6 +824,10 @@ static std::string label(const Node& n) {
     case OpKind::Expand: o << "Expand { shape: " << shape_str(op.shape) << " }"; break;
     case OpKind::Permute: o << "Permute { perm: " << shape_str(op.perm) << " }"; break;
     case OpKind::Sdpa: o << "Sdpa { causal: " << (op.causal ? "true" : "false") << " }"; break;
+    case OpKind::QuantMatmul:
+      o << "QuantMatmul { bits: " << op.qbits << ", group_size: " << op.qgroup << ", symmetric: "
+        << (op.qsym ? "true" : "false") << " }";
+      break;
     case OpKind::DotGeneral:
       o << "DotGeneral { lhs_contract: " << shape_str(op.lc) << ", rhs_contract: " << shape_str(op.rc)
         << ", lhs_batch: " << shape_str(op.lb) << ", rhs_batch: " << shape_str(op.rb) << " }";

@@ -36,6 +36,7 @@ enum class OpKind : uint32_t {
   Softmax, RmsNorm, Sdpa,
   Reshape, Permute, Expand, Slice, Flip, Pad,
   DotGeneral,
+  QuantMatmul,
   NumKinds
 };
 const char* op_name(OpKind k);
@@ -58,6 +59,9 @@ struct Op {
   std::vector<SliceRange> ranges; // Slice
   std::vector<PadRange> pads;     // Pad
   std::vector<size_t> lc, rc, lb, rb;  // DotGeneral: lhs/rhs contract, lhs/rhs batch
+  int qbits = 0;                  // QuantMatmul: 2, 4 or 8
+  size_t qgroup = 0;              // QuantMatmul: K columns per scale group
+  bool qsym = true;               // QuantMatmul: no per-group min
   std::shared_ptr<const std::vector<uint8_t>> data;  // Const payload, little-endian
   DType data_dtype = DType::F32;                     // Const payload dtype
 };
@@ -165,6 +169,11 @@ class Graph {
   NodeId dot_general(NodeId a, NodeId b, const std::vector<size_t>& lc, const std::vector<size_t>& rc,
                      const std::vector<size_t>& lb, const std::vector<size_t>& rb);
   NodeId matmul(NodeId a, NodeId b);
+  // weight-only quantized matmul (graph/ops/core/contract.rs:49-115): act [M, K] float x
+  // dequant(qweight [N, K*bits/8] U8)^T -> [M, N] in act's dtype; scales / mins F16 [N, K/group].
+  // `mins` = KU_ERR-like `kNoNode` for the symmetric form.
+  NodeId quant_matmul(NodeId act, NodeId qweight, NodeId scales, NodeId mins, int bits, size_t group_size);
+  static constexpr NodeId kNoNode = 0xFFFFFFFFu;
 
   // raw append with inference (used by passes)
   NodeId push(Op op, std::vector<NodeId> src);

@@ -12,16 +12,16 @@ namespace {
 constexpr uint8_t kMagic[4] = {'K', 'G', 'P', 'H'};  // serialize.rs:18
 constexpr uint8_t kVersion = 2;                      // serialize.rs:19
 
-// Op tags (encode/op.rs, decode/op.rs:10-87). Tags 0..39 are this IR's OpKind values in
-// declaration order; 40..54 are reference ops outside this IR.
+// Op tags (encode/op.rs, decode/op.rs:10-87). Tags 0..40 are this IR's OpKind values in
+// declaration order; 41..54 are reference ops outside this IR.
 static_assert(static_cast<uint32_t>(OpKind::Const) == 0 && static_cast<uint32_t>(OpKind::Add) == 7 &&
                   static_cast<uint32_t>(OpKind::Sum) == 26 && static_cast<uint32_t>(OpKind::Sdpa) == 32 &&
-                  static_cast<uint32_t>(OpKind::DotGeneral) == 39 && static_cast<uint32_t>(OpKind::NumKinds) == 40,
+                  static_cast<uint32_t>(OpKind::DotGeneral) == 39 &&
+                  static_cast<uint32_t>(OpKind::QuantMatmul) == 40 && static_cast<uint32_t>(OpKind::NumKinds) == 41,
               "OpKind order must match the KGPH v2 op tags");
-const char* const kForeignOps[] = {"QuantMatmul", "Solve", "Det", "Cholesky", "Eigh",
-                                   "Qr", "Eigvals", "Complex", "Real", "Imag",
-                                   "Gather", "Scatter", "GatherAlong", "ScatterAlong", "Argsort"};
-constexpr uint8_t kFirstForeign = 40, kLastTag = 54;
+const char* const kForeignOps[] = {"Solve", "Det", "Cholesky", "Eigh", "Qr", "Eigvals", "Complex",
+                                   "Real", "Imag", "Gather", "Scatter", "GatherAlong", "ScatterAlong", "Argsort"};
+constexpr uint8_t kFirstForeign = 41, kLastTag = 54;
 
 Error fail(const std::string& m) { return Error("deserialize_graph: " + m); }
 
@@ -78,6 +78,7 @@ void write_op(Writer& w, const Op& op) {
       for (const PadRange& p : op.pads) { w.usize(p.lo); w.usize(p.hi); }
       break;
     case OpKind::DotGeneral: w.vec(op.lc); w.vec(op.rc); w.vec(op.lb); w.vec(op.rb); break;
+    case OpKind::QuantMatmul: w.u8((uint8_t)op.qbits); w.usize(op.qgroup); w.boolean(op.qsym); break;
     default: break;  // no attributes
   }
 }
@@ -265,13 +266,16 @@ Op read_op(Reader& r, size_t node) {
       break;
     }
     case OpKind::DotGeneral: op.lc = r.vec(); op.rc = r.vec(); op.lb = r.vec(); op.rb = r.vec(); break;
+    case OpKind::QuantMatmul: op.qbits = r.u8(); op.qgroup = r.usize(); op.qsym = r.boolean(); break;
     default: break;
   }
   return op;
 }
 
-size_t arity(OpKind k) {
+size_t arity(const Op& op) {
+  const OpKind k = op.kind;
   switch (k) {
+    case OpKind::QuantMatmul: return op.qsym ? 3 : 4;  // act, qweight, scales (+ mins)
     case OpKind::Const: case OpKind::Input: case OpKind::Iota: return 0;
     case OpKind::Add: case OpKind::Mul: case OpKind::Max: case OpKind::IDiv: case OpKind::And: case OpKind::Or:
     case OpKind::Xor: case OpKind::Shl: case OpKind::Shr: case OpKind::CmpLt: case OpKind::CmpEq:
@@ -286,8 +290,8 @@ size_t arity(OpKind k) {
 // check of a live graph also guards a decoded one (decode.rs:61 pushes raw and relies on a
 // panic guard instead).
 void replay(Graph& g, size_t i, const Op& op, const std::vector<NodeId>& s) {
-  if (s.size() != arity(op.kind))
-    throw fail("node " + std::to_string(i) + ": " + op_name(op.kind) + " takes " + std::to_string(arity(op.kind)) +
+  if (s.size() != arity(op))
+    throw fail("node " + std::to_string(i) + ": " + op_name(op.kind) + " takes " + std::to_string(arity(op)) +
                " sources, got " + std::to_string(s.size()));
   NodeId got;
   switch (op.kind) {
@@ -341,6 +345,9 @@ void replay(Graph& g, size_t i, const Op& op, const std::vector<NodeId>& s) {
       break;
     }
     case OpKind::DotGeneral: got = g.dot_general(s[0], s[1], op.lc, op.rc, op.lb, op.rb); break;
+    case OpKind::QuantMatmul:
+      got = g.quant_matmul(s[0], s[1], s[2], op.qsym ? Graph::kNoNode : s[3], op.qbits, op.qgroup);
+      break;
     default: throw fail("unknown op tag " + std::to_string(static_cast<uint32_t>(op.kind)));
   }
   if (got != i) throw fail("node " + std::to_string(i) + ": replay recorded extra nodes");

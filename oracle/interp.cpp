@@ -584,6 +584,50 @@ Tensor dot(const Op& op, const Tensor& a, const Tensor& b, const Shape& out_shap
   return from_f32v(dt, out_shape, r);
 }
 
+// quant_matmul (interp/contract.rs:69-99): dequantize the packed weight exactly as
+// quant.rs:100-133 does (raw field, low field first; asymmetric q*s + min, symmetric
+// sign-extended q*s, f16 scale/min widened to f32), then act (cast to f32) x W^T through the
+// f32 contraction above, and the result cast back to act's dtype.
+Tensor quant_matmul(const Op& op, const Tensor& act, const Tensor& qw, const Tensor& scales, const Tensor* mins,
+                    const Shape& out_shape) {
+  const size_t m = act.shape[0], k = act.shape[1], n = qw.shape[0];
+  const int bits = op.qbits;
+  const size_t g = op.qgroup, ng = k / g, rb = k * bits / 8, per = 8 / bits;
+  const uint8_t* pk = qw.bytes.data();
+  auto f16 = [](const Tensor& t, size_t i) {
+    uint16_t h;
+    std::memcpy(&h, t.bytes.data() + 2 * i, 2);
+    return static_cast<float>(f16_to_f64(h));
+  };
+  Tensor w = make(DType::F32, {n, k});
+  float* wp = reinterpret_cast<float*>(w.bytes.data());
+  for (size_t r = 0; r < n; ++r)
+    for (size_t c = 0; c < k; ++c) {
+      const uint32_t raw = (pk[r * rb + c / per] >> ((c % per) * bits)) & ((1u << bits) - 1);
+      const size_t gi = r * ng + c / g;
+      const float s = f16(scales, gi);
+      float v;
+      if (mins) {
+        v = static_cast<float>(raw) * s + f16(*mins, gi);
+      } else {
+        const int sh = 32 - bits;
+        v = static_cast<float>(static_cast<int32_t>(raw << sh) >> sh) * s;
+      }
+      wp[r * k + c] = v;
+    }
+  Tensor af = make(DType::F32, {m, k});
+  {
+    auto x = to_f32v(act);
+    std::memcpy(af.bytes.data(), x.data(), x.size() * 4);
+  }
+  Op d;
+  d.kind = OpKind::DotGeneral;
+  d.lc = {1};
+  d.rc = {1};
+  Tensor r = dot(d, af, w, out_shape);
+  return from_f32v(act.dtype, out_shape, to_f32v(r));
+}
+
 // scale_causal (interp/nn.rs:154-172)
 Tensor scale_causal(const Tensor& raw, float scale, size_t s, bool causal) {
   if (raw.dtype == DType::F64) {
@@ -665,6 +709,7 @@ Tensor eval_op(const Node& n, const std::vector<const Tensor*>& in) {
     case OpKind::Pad:
       return movement(op, *in[0], n.shape);
     case OpKind::DotGeneral: return dot(op, *in[0], *in[1], n.shape);
+    case OpKind::QuantMatmul: return quant_matmul(op, *in[0], *in[1], *in[2], in.size() > 3 ? in[3] : nullptr, n.shape);
     case OpKind::Input: throw std::runtime_error("oracle: Input must come from feeds");
     default: return elementwise(op, n.dtype, in);
   }

@@ -1,0 +1,74 @@
+"""Device parity of Op::QuantMatmul (the fused dequant GEMV for M <= 4, dequantize + GEMM above).
+
+Against the oracle (dequantize, f32 contraction, one rounding to act's dtype) and against an
+f64 product of numpy-dequantized weights: f32 <= 1e-5 normwise; bf16 / f16 <= 1e-2 (the GEMM
+path also rounds each dequantized weight to act's dtype once).
+"""
+import numpy as np
+import pytest
+
+import kurumi_amd as K
+from kurumi_amd import DType, Graph, Tensor
+from kutest import assert_close, interpret, rel_err, to_f32
+from test_quant import dequant
+
+pytestmark = pytest.mark.gpu
+
+
+def build(m, n, k, bits, group, sym, act_dt, seed):
+    rng = np.random.default_rng(seed)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    act = rng.standard_normal((m, k)).astype(np.float32)
+    p, s, mn = K.quantize(w, bits, group, sym)
+    g = Graph()
+    x = g.input([m, k], act_dt)
+    qw = g.constant_bytes(DType.U8, p.tobytes(), p.shape)
+    sc = g.constant_bytes(DType.F16, s.tobytes(), s.shape)
+    mnn = None if mn is None else g.constant_bytes(DType.F16, mn.tobytes(), mn.shape)
+    y = g.quant_matmul(x, qw, sc, mnn, bits, group)
+    if act_dt == DType.F32:
+        xt = Tensor.from_numpy(act)
+    else:
+        xt = interpret(*(lambda gg: (gg, [gg.cast(gg.constant(act), act_dt)]))(Graph()))[0]
+    truth = to_f32(xt).astype(np.float64) @ dequant(p, s, mn, k, bits, group).astype(np.float64).T
+    return g, x, y, xt, truth
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 17, 64])
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("sym", [True, False])
+@pytest.mark.parametrize("act_dt", [DType.F32, DType.BF16])
+def test_quant_matmul_matches_oracle(hip, m, bits, sym, act_dt):
+    print(f"quant m={m} bits={bits} sym={sym} {act_dt.name}", flush=True)
+    g, x, y, xt, truth = build(m, 96, 256, bits, 64, sym, act_dt, 100 + m + bits)
+    feeds = {x: xt}
+    got = to_f32(hip.eval_with(g, y, feeds))
+    want = to_f32(interpret(g, [y], feeds)[0])
+    tol = 1e-5 if act_dt == DType.F32 else 1e-2
+    assert rel_err(got, truth) <= tol, rel_err(got, truth)
+    assert_close(got, want, rtol=tol, atol=tol * np.abs(want).max(), what="quant vs oracle")
+
+
+@pytest.mark.parametrize("k,group,bits", [(40, 8, 4), (24, 24, 8), (64, 16, 2), (96, 96, 4)])
+def test_quant_gemv_odd_rows_and_groups(hip, k, group, bits):
+    """Rows that are not whole 16-byte chunks, and groups smaller than a chunk's fields."""
+    print(f"quant odd k={k} g={group} bits={bits}", flush=True)
+    for m in (1, 3):
+        g, x, y, xt, truth = build(m, 37, k, bits, group, False, DType.F32, 7 + k)
+        got = hip.eval_with(g, y, {x: xt}).numpy()
+        assert rel_err(got, truth) <= 1e-5
+
+
+def test_quant_f16_act(hip):
+    g, x, y, xt, truth = build(2, 64, 128, 4, 32, True, DType.F16, 9)
+    got = to_f32(hip.eval_with(g, y, {x: xt}))
+    assert rel_err(got, truth) <= 1e-2
+
+
+def test_quant_decode_full_size(hip):
+    """The decode shape: one token through an int4 (group 128) [11008, 4096] projection, bf16."""
+    print("quant decode 1x4096 -> 11008", flush=True)
+    g, x, y, xt, truth = build(1, 11008, 4096, 4, 128, True, DType.BF16, 11)
+    got = to_f32(hip.eval_with(g, y, {x: xt}))
+    assert rel_err(got, truth) <= 1e-2
+    assert_close(got, truth, rtol=1e-2, atol=1e-2 * np.abs(truth).max(), what="decode")

@@ -172,7 +172,7 @@ def test_multi_entry_round_trips():
 
 
 def every_op_graph():
-    """A graph holding each of the 40 op kinds of this IR at least once."""
+    """A graph holding each of the 41 op kinds of this IR at least once."""
     g = Graph()
     x = g.input([2, 4], DType.F32)
     xi = g.input([2, 4], DType.I32)
@@ -195,6 +195,12 @@ def every_op_graph():
     outs += [g.reshape(x, [4, 2]), g.permute(x, [1, 0]), g.expand(g.reshape(x, [2, 1, 4]), [2, 3, 4])]
     outs += [g.slice_step(x, [(0, 2, 1), (1, 4, 2)]), g.flip(x, [0, 1]), g.pad(x, [(1, 0), (0, 2)])]
     outs.append(g.dot_general(x, c, [1], [1], [0], [0]))
+    packed, scales, mins = K.quantize(np.arange(32, dtype=np.float32).reshape(4, 8), 4, 8, False)
+    qw = g.constant_bytes(DType.U8, packed.tobytes(), packed.shape)
+    sc = g.constant_bytes(DType.F16, scales.tobytes(), scales.shape)
+    mn = g.constant_bytes(DType.F16, mins.tobytes(), mins.shape)
+    xq = g.reshape(x, [1, 8])
+    outs += [g.quant_matmul(xq, qw, sc, mn, 4, 8), g.quant_matmul(xq, qw, sc, None, 4, 8)]
     return g, outs
 
 
@@ -204,7 +210,7 @@ def test_every_op_round_trips():
     r = K.deserialize_graph(blob)
     assert K.serialize_graph(r.graph, r.outputs) == blob  # encode(decode(b)) == b
     kinds = set(blob_op_tags(blob))
-    assert kinds == set(range(40)), sorted(set(range(40)) - kinds)
+    assert kinds == set(range(41)), sorted(set(range(41)) - kinds)
     for o in outs:
         assert r.graph.shape(o) == g.shape(o) and r.graph.dtype(o) == g.dtype(o)
 
@@ -255,6 +261,8 @@ def node_end(b: bytes, p: int) -> int:
     elif tag == 39:
         for _ in range(4):
             p = vec(p)
+    elif tag == 40:
+        p += 10
     ns = struct.unpack_from("<I", b, p)[0]
     return p + 4 + 4 * ns
 
@@ -305,7 +313,7 @@ def test_rejects_entryless_blob_and_bad_fields():
     rejects(header(1) + const_f32([1.0], [1]) + struct.pack("<I", 0), "no entries")
     rejects(header(1) + b"\x00\x63", "unknown dtype tag 99")
     rejects(header(1) + b"\x63", "unknown op tag 99")
-    rejects(header(1) + b"\x28\x04" + struct.pack("<QB", 32, 1), r"QuantMatmul \(tag 40\)")
+    rejects(header(1) + b"\x29", r"Solve \(tag 41\)")
     body = header(1) + const_f32([1.0, 2.0], [2])
     rejects(body + struct.pack("<I", 1) + struct.pack("<IIII", 0, 1, 0, 1) + struct.pack("<IBI", 0, 2, 0),
             "bad input role 2")
