@@ -28,7 +28,7 @@ namespace {
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
-constexpr int GEMV_RW = 8;  // weight rows per work-group
+constexpr int GEMV_RW = 4;  // weight rows per work-group (4 measured best for the decode shape)
 
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
@@ -186,6 +186,122 @@ __global__ void __launch_bounds__(256) quant_gemv_k(QuantArgs a) {
   }
 }
 
+// Fast path of quant_gemv_k (chunks of 16 packed bytes, 8 for int2; each chunk inside one scale
+// group). The fields are turned into floats a byte at a time with v_cvt_f32_ubyte{0..3} after one
+// mask per word, and the per-value scale is factored out of the chunk's sum:
+//   sum_e act[e] * w[e] = s * (sum_e act[e] * u[e] - off * sum_e act[e]) + min * sum_e act[e]
+// with u the unsigned field (symmetric fields are offset by 2^(bits-1) with one xor per word,
+// off = 2^(bits-1); asymmetric: off = 0). The act sums are shared by all rows of the work-group.
+// This reassociates the f32 arithmetic of the reference's per-value dequantisation (a few f32
+// ulps of the chunk sum), well inside the f32 tolerance.
+template <int BITS, bool SYM, int AT, int MB>
+__global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
+  constexpr int CB = BITS == 2 ? 8 : 16, PER = 8 / BITS, E = CB * PER, NWD = CB / 4;
+  constexpr int VW = 4 * PER;                 // values per 32-bit word
+  constexpr int V = VW < 8 ? 8 : VW;          // act values loaded at a time (whole words)
+  constexpr uint32_t FMASK = BITS == 8 ? 0xFFFFFFFFu : (BITS == 4 ? 0x0F0F0F0Fu : 0x03030303u);
+  constexpr uint32_t XOR = SYM ? (BITS == 8 ? 0x80808080u : (BITS == 4 ? 0x88888888u : 0xAAAAAAAAu)) : 0u;
+  constexpr float OFF = SYM ? (float)(1 << (BITS - 1)) : 0.f;
+  __shared__ float red[4][GEMV_RW * MB];
+  const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6, nwv = nt >> 6;
+  const int64_t K = a.k, N = a.n, rb = K * BITS / 8, ng = K / a.group, nch = K / E;
+  const int64_t row0 = (int64_t)blockIdx.x * GEMV_RW;
+  int64_t rows[GEMV_RW];
+#pragma unroll
+  for (int r = 0; r < GEMV_RW; ++r) rows[r] = row0 + r < N ? row0 + r : N - 1;  // duplicates never stored
+  float acc[GEMV_RW][MB];
+#pragma unroll
+  for (int r = 0; r < GEMV_RW; ++r)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) acc[r][m] = 0.f;
+  for (int64_t c = tid; c < nch; c += nt) {
+    const int64_t k = c * E;
+    uint32_t wb[GEMV_RW][NWD];
+#pragma unroll
+    for (int r = 0; r < GEMV_RW; ++r) {
+      const uint8_t* p = a.qw + rows[r] * rb + k / PER;
+      if constexpr (CB == 16) {
+        const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wb[r][j] = w[j] ^ XOR;
+      } else {
+        const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+        wb[r][0] = w[0] ^ XOR;
+        wb[r][1] = w[1] ^ XOR;
+      }
+    }
+    float s[GEMV_RW], mn[GEMV_RW];
+    const uint32_t kg = (uint32_t)k / (uint32_t)a.group;  // one 32-bit division per chunk
+#pragma unroll
+    for (int r = 0; r < GEMV_RW; ++r) {
+      const uint32_t gi = (uint32_t)rows[r] * (uint32_t)ng + kg;
+      s[r] = f16_to_f32(a.scales[gi]);
+      mn[r] = SYM ? 0.f : f16_to_f32(a.mins[gi]);
+    }
+    float part[GEMV_RW][MB], asum[MB];
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      asum[m] = 0.f;
+#pragma unroll
+      for (int r = 0; r < GEMV_RW; ++r) part[r][m] = 0.f;
+    }
+#pragma unroll
+    for (int e0 = 0; e0 < E; e0 += V) {
+      float av[MB][V];
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        if (m < a.m) load_act<AT, V>(a.act, m * K + k + e0, av[m]);
+        else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) av[m][e] = 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) asum[m] += av[m][e];
+      }
+#pragma unroll
+      for (int r = 0; r < GEMV_RW; ++r)
+#pragma unroll
+        for (int wi = 0; wi < V / VW; ++wi) {
+          const uint32_t word = wb[r][e0 / VW + wi];
+#pragma unroll
+          for (int f = 0; f < PER; ++f) {
+            const uint32_t fw = (word >> (f * BITS)) & FMASK;  // field f of each of the 4 bytes
+#pragma unroll
+            for (int bj = 0; bj < 4; ++bj) {
+              const float u = (float)((fw >> (8 * bj)) & 0xFFu);  // v_cvt_f32_ubyte{bj}
+              const int e = wi * VW + bj * PER + f;
+#pragma unroll
+              for (int m = 0; m < MB; ++m) part[r][m] = fmaf(av[m][e], u, part[r][m]);
+            }
+          }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < GEMV_RW; ++r)
+#pragma unroll
+      for (int m = 0; m < MB; ++m) {
+        const float q = SYM ? fmaf(-OFF, asum[m], part[r][m]) : part[r][m];
+        acc[r][m] = fmaf(s[r], q, acc[r][m]);
+        if constexpr (!SYM) acc[r][m] = fmaf(mn[r], asum[m], acc[r][m]);
+      }
+  }
+#pragma unroll
+  for (int r = 0; r < GEMV_RW; ++r)
+#pragma unroll
+    for (int m = 0; m < MB; ++m) {
+      const float v = wave_add(acc[r][m]);
+      if (lane == 0) red[wave][r * MB + m] = v;
+    }
+  __syncthreads();
+  if (tid < GEMV_RW * MB) {
+    const int r = tid / MB, m = tid % MB;
+    float v = red[0][tid];
+    for (int w = 1; w < nwv; ++w) v += red[w][tid];
+    const int64_t n = row0 + r;
+    if (n < N && m < a.m) act_st<AT>(a.out, m * N + n, v);
+  }
+}
+
 // one thread per packed byte of the weight: its 8/BITS values into wdq [N, K] (dtype WT)
 template <int BITS, bool SYM, int WT>
 __global__ void __launch_bounds__(256) quant_dequant_k(QuantArgs a) {
@@ -215,7 +331,7 @@ void gemv_mb(const QuantArgs& a, hipStream_t s) {
   const int64_t nch = kind == 0 ? rb / CB : rb;
   const int nwv = (int)std::min<int64_t>(4, std::max<int64_t>(1, (nch + 63) / 64));
   const dim3 grid((unsigned)((a.n + GEMV_RW - 1) / GEMV_RW)), block((unsigned)(nwv * 64));
-  if (kind == 0) hipLaunchKernelGGL((quant_gemv_k<BITS, SYM, AT, MB, CB, true>), grid, block, 0, s, a);
+  if (kind == 0) hipLaunchKernelGGL((quant_gemv_fast_k<BITS, SYM, AT, MB>), grid, block, 0, s, a);
   else if (kind == 1) hipLaunchKernelGGL((quant_gemv_k<BITS, SYM, AT, MB, 1, true>), grid, block, 0, s, a);
   else hipLaunchKernelGGL((quant_gemv_k<BITS, SYM, AT, MB, 1, false>), grid, block, 0, s, a);
 }
@@ -264,6 +380,8 @@ bool quant_gemv_ok(const QuantArgs& a) { return a.m >= 1 && a.m <= 4; }
 
 void launch_quant_gemv(const QuantArgs& a, hipStream_t s) {
   check(a);
+  if (a.n * (a.k / a.group) >= (int64_t(1) << 31) || a.k >= (int64_t(1) << 31))
+    throw std::runtime_error("quant: scale table or K too large for the GEMV kernel's 32-bit indices");
   if (!quant_gemv_ok(a)) throw std::runtime_error("quant: the GEMV kernel takes M <= 4");
   if (a.n == 0) return;
   if (reinterpret_cast<uintptr_t>(a.qw) & 15)
