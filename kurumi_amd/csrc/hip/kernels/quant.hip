@@ -5,9 +5,11 @@
 // min when asymmetric (w = q * s + min) or a sign-extended field when symmetric (w = q * s);
 // f32 products and accumulation, the result rounded once to act's dtype.
 //
-// quant_gemv_k (M <= 4, the decode shapes): the weight is read from HBM exactly once and
-// dequantized in registers; eight weight rows per work-group share each act value a thread
-// loads, and their 16-byte chunks are all in flight at once.
+// quant_gemv_fast_k / quant_gemv_k (M <= 4, the decode shapes): the weight is read from HBM
+// exactly once and dequantized in registers; GEMV_RW weight rows per work-group share each act
+// value a thread loads, and their 16-byte chunks are all in flight at once. With bf16 / f16 act
+// and 2- or 4-bit fields the products run on v_dot2 pairs (one v_bitop3 turns two fields into a
+// 16-bit pair), which keeps the VALU work per weight byte below the HBM time.
 // quant_dequant_k (M > 4): the weight is expanded once into act's dtype (f32, bf16 or f16) for
 // the MFMA / generic GEMM; bf16 / f16 round each dequantized weight once, the f32 products then
 // accumulate in f32 like the reference.
@@ -58,10 +60,32 @@ __device__ __forceinline__ float deq(uint32_t raw, float s, float mn) {
   }
 }
 
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// sum over the wave, valid in every lane: DPP row shifts, then row broadcasts into lane 63
+// (VALU latency per step, no LDS permutes)
 __device__ __forceinline__ float wave_add(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f<0x111, 0xf>(v);  // row_shr:1
+  v += dpp_f<0x112, 0xf>(v);  // row_shr:2
+  v += dpp_f<0x114, 0xf>(v);  // row_shr:4
+  v += dpp_f<0x118, 0xf>(v);  // row_shr:8: lane 15 of each row of 16 holds the row's sum
+  v += dpp_f<0x142, 0xa>(v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f<0x143, 0xc>(v);  // row_bcast:31 into rows 2 and 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// acc + lo(x) * lo(y) + hi(x) * hi(y) on 16-bit pairs (bf16 or f16), f32 accumulate
+template <int AT>
+__device__ __forceinline__ float dot2(uint32_t x, uint32_t y, float acc) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+  if constexpr (AT == GT_BF16)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), __builtin_bit_cast(bf16x2, y), acc, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), __builtin_bit_cast(f16x2, y), acc, false);
 }
 
 // V consecutive act values of one row as f32 (one or two 16-byte loads when V allows)
@@ -202,6 +226,16 @@ __global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
   constexpr uint32_t FMASK = BITS == 8 ? 0xFFFFFFFFu : (BITS == 4 ? 0x0F0F0F0Fu : 0x03030303u);
   constexpr uint32_t XOR = SYM ? (BITS == 8 ? 0x80808080u : (BITS == 4 ? 0x88888888u : 0xAAAAAAAAu)) : 0u;
   constexpr float OFF = SYM ? (float)(1 << (BITS - 1)) : 0.f;
+  // 16-bit act (bf16 / f16) with 2- or 4-bit fields: v_dot2 on pairs. A field u (< 16) OR-ed into
+  // the mantissa of MAGICV (128 in bf16, 1024 in f16, both with ulp 1) is exactly MAGICV + u, and
+  // the MAGICV * sum(act) this adds is taken off with the offset.
+  constexpr bool DOT = BITS != 8 && AT != GT_F32;
+  constexpr int H = VW / 2;
+  constexpr uint32_t PMASK = BITS == 4 ? 0x000F000Fu : 0x00030003u;
+  constexpr uint32_t MAGIC = AT == GT_BF16 ? 0x43004300u : 0x64006400u;
+  constexpr float MAGICV = AT == GT_BF16 ? 128.f : 1024.f;
+  constexpr uint32_t LXOR = DOT ? 0u : XOR;  // the dot path applies the offset in its v_bitop3
+  constexpr uint32_t ONES = AT == GT_BF16 ? 0x3F803F80u : 0x3C003C00u;
   __shared__ float red[4][GEMV_RW * MB];
   const int tid = threadIdx.x, nt = blockDim.x, lane = tid & 63, wave = tid >> 6, nwv = nt >> 6;
   const int64_t K = a.k, N = a.n, rb = K * BITS / 8, ng = K / a.group, nch = K / E;
@@ -223,11 +257,11 @@ __global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
       if constexpr (CB == 16) {
         const u32x4 w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) wb[r][j] = w[j] ^ XOR;
+        for (int j = 0; j < 4; ++j) wb[r][j] = w[j] ^ LXOR;
       } else {
         const u32x2 w = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-        wb[r][0] = w[0] ^ XOR;
-        wb[r][1] = w[1] ^ XOR;
+        wb[r][0] = w[0] ^ LXOR;
+        wb[r][1] = w[1] ^ LXOR;
       }
     }
     float s[GEMV_RW], mn[GEMV_RW];
@@ -244,6 +278,59 @@ __global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
       asum[m] = 0.f;
 #pragma unroll
       for (int r = 0; r < GEMV_RW; ++r) part[r][m] = 0.f;
+    }
+    if constexpr (DOT) {
+      // act as raw 16-bit pairs: E values = E / 2 words per row of act
+      uint32_t aw[MB][E / 2];
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int q = 0; q < E / 8; ++q) {
+          const u32x4 v = m < a.m ? *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.act) + m * K + k + 8 * q)
+                                  : u32x4{0, 0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) aw[m][4 * q + i] = v[i];
+        }
+#pragma unroll
+      for (int m = 0; m < MB; ++m)
+#pragma unroll
+        for (int i = 0; i < E / 2; ++i) asum[m] = dot2<AT>(aw[m][i], ONES, asum[m]);
+#pragma unroll
+      for (int wi = 0; wi < NWD; ++wi) {
+        // pair p of word wi: fields p (low half) and p + H (high half), values wi*VW + p, + p + H
+        uint32_t ap[MB][H];
+#pragma unroll
+        for (int m = 0; m < MB; ++m)
+#pragma unroll
+          for (int p = 0; p < H; ++p) {
+            // e_lo and e_hi = e_lo + H (H even) sit in the same half of their act words
+            const int e_lo = wi * VW + p, e_hi = e_lo + H;
+            constexpr uint32_t SEL[2] = {0x05040100u, 0x07060302u};  // v_perm_b32: half h of src1 | half h of src0
+            ap[m][p] = __builtin_amdgcn_perm(aw[m][e_hi >> 1], aw[m][e_lo >> 1], SEL[e_lo & 1]);
+          }
+#pragma unroll
+        for (int r = 0; r < GEMV_RW; ++r) {
+          const uint32_t word = wb[r][wi];
+#pragma unroll
+          for (int p = 0; p < H; ++p) {
+            // (MAGICV + u) as a 16-bit pair: C ^ (t & PMASK) with C = MAGIC | XOR in one v_bitop3
+            // (0x6c: S1 ^ (S0 & S2)); the symmetric offset's xor rides along
+            uint32_t x;
+            asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6c" : "=v"(x) : "v"(word >> (BITS * p)), "v"(MAGIC | (XOR & PMASK)), "v"(PMASK));
+#pragma unroll
+            for (int m = 0; m < MB; ++m) part[r][m] = dot2<AT>(x, ap[m][p], part[r][m]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < GEMV_RW; ++r)
+#pragma unroll
+        for (int m = 0; m < MB; ++m) {
+          const float q = fmaf(-(MAGICV + OFF), asum[m], part[r][m]);
+          acc[r][m] = fmaf(s[r], q, acc[r][m]);
+          if constexpr (!SYM) acc[r][m] = fmaf(mn[r], asum[m], acc[r][m]);
+        }
+      continue;
     }
 #pragma unroll
     for (int e0 = 0; e0 < E; e0 += V) {

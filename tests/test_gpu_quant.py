@@ -59,10 +59,17 @@ def test_quant_gemv_odd_rows_and_groups(hip, k, group, bits):
         assert rel_err(got, truth) <= 1e-5
 
 
-def test_quant_f16_act(hip):
-    g, x, y, xt, truth = build(2, 64, 128, 4, 32, True, DType.F16, 9)
-    got = to_f32(hip.eval_with(g, y, {x: xt}))
-    assert rel_err(got, truth) <= 1e-2
+@pytest.mark.parametrize("bits", [2, 4, 8])
+@pytest.mark.parametrize("sym", [True, False])
+def test_quant_f16_act(hip, bits, sym):
+    """f16 act (the v_dot2_f32_f16 path for 2- and 4-bit fields, whose 1024 + u trick has the
+    largest cancellation), M = 1 .. 3."""
+    for m in (1, 3):
+        g, x, y, xt, truth = build(m, 64, 256, bits, 32, sym, DType.F16, 9 + bits + m)
+        got = to_f32(hip.eval_with(g, y, {x: xt}))
+        assert rel_err(got, truth) <= 1e-2
+        want = to_f32(interpret(g, [y], {x: xt})[0])
+        assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="f16 quant vs oracle")
 
 
 def test_quant_decode_full_size(hip):
