@@ -5,12 +5,12 @@
 // min when asymmetric (w = q * s + min) or a sign-extended field when symmetric (w = q * s);
 // f32 products and accumulation, the result rounded once to act's dtype.
 //
-// quant_gemv_fast_k / quant_gemv_k (M <= 4, the decode shapes): the weight is read from HBM
+// quant_gemv_fast_k / quant_gemv_k (M <= 8, the decode shapes): the weight is read from HBM
 // exactly once and dequantized in registers; GEMV_RW weight rows per work-group share each act
 // value a thread loads, and their 16-byte chunks are all in flight at once. With bf16 / f16 act
 // and 2- or 4-bit fields the products run on v_dot2 pairs (one v_bitop3 turns two fields into a
 // 16-bit pair), which keeps the VALU work per weight byte below the HBM time.
-// quant_dequant_k (M > 4): the weight is expanded once into act's dtype (f32, bf16 or f16) for
+// quant_dequant_k (M > 8): the weight is expanded once into act's dtype (f32, bf16 or f16) for
 // the MFMA / generic GEMM; bf16 / f16 round each dequantized weight once, the f32 products then
 // accumulate in f32 like the reference.
 #include <hip/hip_runtime.h>
@@ -280,33 +280,41 @@ __global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
       for (int r = 0; r < GEMV_RW; ++r) part[r][m] = 0.f;
     }
     if constexpr (DOT) {
-      // act as raw 16-bit pairs: E values = E / 2 words per row of act
-      uint32_t aw[MB][E / 2];
+      // act as raw 16-bit pairs, VW / 2 words per weight word and act row: the whole chunk's act
+      // loaded up front for M <= 4 (measured faster), one weight word's at a time for M = 8
+      // (registers)
+      constexpr int AWW = MB <= 4 ? NWD : 1;
+      uint32_t awc[MB][AWW * VW / 2];
+      auto load_aw = [&](int w0) {
 #pragma unroll
-      for (int m = 0; m < MB; ++m)
+        for (int m = 0; m < MB; ++m)
 #pragma unroll
-        for (int q = 0; q < E / 8; ++q) {
-          const u32x4 v = m < a.m ? *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.act) + m * K + k + 8 * q)
-                                  : u32x4{0, 0, 0, 0};
+          for (int q = 0; q < AWW * VW / 8; ++q) {
+            const u32x4 v = m < a.m ? *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.act) + m * K + k +
+                                                                      w0 * VW + 8 * q)
+                                    : u32x4{0, 0, 0, 0};
 #pragma unroll
-          for (int i = 0; i < 4; ++i) aw[m][4 * q + i] = v[i];
-        }
+            for (int i = 0; i < 4; ++i) awc[m][4 * q + i] = v[i];
+          }
 #pragma unroll
-      for (int m = 0; m < MB; ++m)
+        for (int m = 0; m < MB; ++m)
 #pragma unroll
-        for (int i = 0; i < E / 2; ++i) asum[m] = dot2<AT>(aw[m][i], ONES, asum[m]);
+          for (int i = 0; i < AWW * VW / 2; ++i) asum[m] = dot2<AT>(awc[m][i], ONES, asum[m]);
+      };
+      if constexpr (AWW == NWD) load_aw(0);
 #pragma unroll
       for (int wi = 0; wi < NWD; ++wi) {
-        // pair p of word wi: fields p (low half) and p + H (high half), values wi*VW + p, + p + H
+        if constexpr (AWW == 1) load_aw(wi);
+        const int wb0 = AWW == 1 ? 0 : wi * VW / 2;  // word wi's first act word in awc
+        // pair p of word wi: fields p (low half) and p + H (high half), act values p and p + H
         uint32_t ap[MB][H];
 #pragma unroll
         for (int m = 0; m < MB; ++m)
 #pragma unroll
           for (int p = 0; p < H; ++p) {
-            // e_lo and e_hi = e_lo + H (H even) sit in the same half of their act words
-            const int e_lo = wi * VW + p, e_hi = e_lo + H;
+            // p and p + H (H even) sit in the same half of their act words
             constexpr uint32_t SEL[2] = {0x05040100u, 0x07060302u};  // v_perm_b32: half h of src1 | half h of src0
-            ap[m][p] = __builtin_amdgcn_perm(aw[m][e_hi >> 1], aw[m][e_lo >> 1], SEL[e_lo & 1]);
+            ap[m][p] = __builtin_amdgcn_perm(awc[m][wb0 + ((p + H) >> 1)], awc[m][wb0 + (p >> 1)], SEL[p & 1]);
           }
 #pragma unroll
         for (int r = 0; r < GEMV_RW; ++r) {
@@ -428,7 +436,9 @@ void gemv_at(const QuantArgs& a, hipStream_t s) {
   switch (a.m) {
     case 1: gemv_mb<BITS, SYM, AT, 1>(a, s); return;
     case 2: gemv_mb<BITS, SYM, AT, 2>(a, s); return;
-    default: gemv_mb<BITS, SYM, AT, 4>(a, s); return;
+    case 3:
+    case 4: gemv_mb<BITS, SYM, AT, 4>(a, s); return;
+    default: gemv_mb<BITS, SYM, AT, 8>(a, s); return;
   }
 }
 
@@ -463,13 +473,13 @@ void check(const QuantArgs& a) {
 
 }  // namespace
 
-bool quant_gemv_ok(const QuantArgs& a) { return a.m >= 1 && a.m <= 4; }
+bool quant_gemv_ok(const QuantArgs& a) { return a.m >= 1 && a.m <= 8; }
 
 void launch_quant_gemv(const QuantArgs& a, hipStream_t s) {
   check(a);
   if (a.n * (a.k / a.group) >= (int64_t(1) << 31) || a.k >= (int64_t(1) << 31))
     throw std::runtime_error("quant: scale table or K too large for the GEMV kernel's 32-bit indices");
-  if (!quant_gemv_ok(a)) throw std::runtime_error("quant: the GEMV kernel takes M <= 4");
+  if (!quant_gemv_ok(a)) throw std::runtime_error("quant: the GEMV kernel takes M <= 8");
   if (a.n == 0) return;
   if (reinterpret_cast<uintptr_t>(a.qw) & 15)
     throw std::runtime_error("quant: packed weight must be 16-byte aligned");

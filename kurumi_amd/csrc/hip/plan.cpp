@@ -1051,7 +1051,8 @@ void Planner::visit_quant(NodeId id) {
   Q.act_dtype = at;
   Q.wdq_dtype = at;  // bf16 / f16 act: the MFMA GEMM on rounded weights; f32: the generic GEMM
   Q.out_slot = new_slot(SlotKind::Temp, at, Q.m * Q.n * dt_width(at), id);
-  if (!(Q.m >= 1 && Q.m <= 4)) Q.wdq_slot = new_slot(SlotKind::Temp, Q.wdq_dtype, Q.n * Q.k * dt_width(Q.wdq_dtype), id);
+  // M <= 8: the fused dequant GEMV (quant_gemv_ok); above: dequantise once + GEMM
+  if (!(Q.m >= 1 && Q.m <= 8)) Q.wdq_slot = new_slot(SlotKind::Temp, Q.wdq_dtype, Q.n * Q.k * dt_width(Q.wdq_dtype), id);
   P_.quants_.push_back(Q);
   int step = new_step(Step::QUANT, (int)P_.quants_.size() - 1, "quant");
   for (int i = 0; i < 4; ++i)

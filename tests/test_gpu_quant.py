@@ -1,4 +1,4 @@
-"""Device parity of Op::QuantMatmul (the fused dequant GEMV for M <= 4, dequantize + GEMM above).
+"""Device parity of Op::QuantMatmul (the fused dequant GEMV for M <= 8, dequantize + GEMM above).
 
 Against the oracle (dequantize, f32 contraction, one rounding to act's dtype) and against an
 f64 product of numpy-dequantized weights: f32 <= 1e-5 normwise; bf16 / f16 <= 1e-2 (the GEMM
@@ -34,7 +34,7 @@ def build(m, n, k, bits, group, sym, act_dt, seed):
     return g, x, y, xt, truth
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 17, 64])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 9, 17, 64])
 @pytest.mark.parametrize("bits", [2, 4, 8])
 @pytest.mark.parametrize("sym", [True, False])
 @pytest.mark.parametrize("act_dt", [DType.F32, DType.BF16])
@@ -53,7 +53,7 @@ def test_quant_matmul_matches_oracle(hip, m, bits, sym, act_dt):
 def test_quant_gemv_odd_rows_and_groups(hip, k, group, bits):
     """Rows that are not whole 16-byte chunks, and groups smaller than a chunk's fields."""
     print(f"quant odd k={k} g={group} bits={bits}", flush=True)
-    for m in (1, 3):
+    for m in (1, 3, 7):
         g, x, y, xt, truth = build(m, 37, k, bits, group, False, DType.F32, 7 + k)
         got = hip.eval_with(g, y, {x: xt}).numpy()
         assert rel_err(got, truth) <= 1e-5

@@ -175,7 +175,8 @@ def test_quant_matmul_record_time_errors():
 def test_plan_labels_gemv_and_gemm_paths():
     rng = np.random.default_rng(3)
     p, s, mn = K.quantize(rng.standard_normal((64, 128)).astype(np.float32), 4, 32, True)
-    for m, want in ((1, "quant_gemv int4s g32 m1 n64 k128"), (4, "quant_gemv"), (16, "quant_dequant+gemm")):
+    for m, want in ((1, "quant_gemv int4s g32 m1 n64 k128"), (4, "quant_gemv"), (8, "quant_gemv"), (9, "quant_dequant+gemm"),
+                    (16, "quant_dequant+gemm")):
         g, y = quant_graph(rng.standard_normal((m, 128)).astype(np.float32), p, s, mn, 4, 32, DType.BF16)
         src = g.codegen([y])
         steps = [l.split(": ", 1)[1] for l in src.splitlines() if l.startswith("// step ")]
