@@ -81,6 +81,7 @@ __global__ void __launch_bounds__(256) gemm_generic_k(GemmArgs a) {
           if (a.col_scale) f *= a.col_scale[gn * a.col_scale_stride];
           v = (TA)f;
         }
+        if constexpr (std::is_same_v<TA, float>) v = d_round_through(a.round_type, v);  // fused cast
         C[gm * a.n + gn] = store_elem<OT, TO, TA>(v);
       }
     }

@@ -308,6 +308,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
   // after the loop's last barrier) and written back row-contiguous, 16 bytes per lane and 128
   // bytes per row and instruction.
   const float alpha = a.alpha ? a.alpha[0] : 1.f;
+  const int rt = a.round_type;  // a fused cast from the contraction's 16-bit dtype
   void* C = static_cast<unsigned char*>(a.c) + bz * a.m * a.n * (OT == GT_F32 ? 4 : 2);
   const int64_t rbase = m0 + wm * TM, cbase = n0 + wn * TN;
   float cs[FN][4][4];  // column scales of this lane's columns
@@ -334,17 +335,20 @@ __global__ void __launch_bounds__(WM* WN * 64)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int u = j * 8 + g * 2 + h;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = acc[i][j][4 * g + e] * cs[j][g][e];
+          if (rt >= 0) {  // uniform branch
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = d_round_through(rt, v[e]);
+          }
           u32x2 w;
           if constexpr (OT == GT_BF16) {
-            w[0] = (uint32_t)d_bf16_st(acc[i][j][4 * g] * cs[j][g][0]) |
-                   ((uint32_t)d_bf16_st(acc[i][j][4 * g + 1] * cs[j][g][1]) << 16);
-            w[1] = (uint32_t)d_bf16_st(acc[i][j][4 * g + 2] * cs[j][g][2]) |
-                   ((uint32_t)d_bf16_st(acc[i][j][4 * g + 3] * cs[j][g][3]) << 16);
+            w[0] = (uint32_t)d_bf16_st(v[0]) | ((uint32_t)d_bf16_st(v[1]) << 16);
+            w[1] = (uint32_t)d_bf16_st(v[2]) | ((uint32_t)d_bf16_st(v[3]) << 16);
           } else {
-            w[0] = (uint32_t)d_f16_st(acc[i][j][4 * g] * cs[j][g][0]) |
-                   ((uint32_t)d_f16_st(acc[i][j][4 * g + 1] * cs[j][g][1]) << 16);
-            w[1] = (uint32_t)d_f16_st(acc[i][j][4 * g + 2] * cs[j][g][2]) |
-                   ((uint32_t)d_f16_st(acc[i][j][4 * g + 3] * cs[j][g][3]) << 16);
+            w[0] = (uint32_t)d_f16_st(v[0]) | ((uint32_t)d_f16_st(v[1]) << 16);
+            w[1] = (uint32_t)d_f16_st(v[2]) | ((uint32_t)d_f16_st(v[3]) << 16);
           }
           *(KU_LDS u32x2*)(EP + r * ROWB + ((u ^ ((r >> 1) & 15)) << 3)) = w;
         }
@@ -381,7 +385,8 @@ __global__ void __launch_bounds__(WM* WN * 64)
           const int64_t col = cbase + j * 32 + g * 8 + h * 4;
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (col + e < a.n) static_cast<float*>(C)[row * a.n + col + e] = acc[i][j][4 * g + e] * cs[j][g][e];
+            if (col + e < a.n)
+              static_cast<float*>(C)[row * a.n + col + e] = d_round_through(rt, acc[i][j][4 * g + e] * cs[j][g][e]);
         }
     }
   }

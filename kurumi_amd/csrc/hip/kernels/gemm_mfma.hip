@@ -247,7 +247,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int64_t row = m0 + wm * TM + i * 32 + (v >> 2) * 8 + (lane >> 5) * 4 + (v & 3);
-        if (row < a.m) store_out<OT>(C, row * a.n + col, acc[i][j][v] * cs);
+        if (row < a.m) store_out<OT>(C, row * a.n + col, d_round_through(a.round_type, acc[i][j][v] * cs));
       }
     }
   }

@@ -23,6 +23,9 @@ struct GemmArgs {
   const float* alpha = nullptr;
   const float* col_scale = nullptr;
   int64_t col_scale_stride = 1;
+  // optional fused cast: the (scaled) f32 result is first rounded to this 16-bit float type (the
+  // contraction's own dtype, GT_BF16 / GT_F16), then converted to out_type; -1: no extra rounding
+  int round_type = -1;
 };
 
 // Returns a short name of the kernel variant that will run (for plan labels).

@@ -43,6 +43,13 @@ __device__ __forceinline__ uint8_t d_e5m2_st(float x) {
   return (uint8_t)(__builtin_amdgcn_cvt_pk_bf8_f32(x, 0.f, 0, false) & 0xffu);
 }
 
+// round an f32 value to bf16 / f16 and back (a fused cast's source dtype); rt < 0: unchanged
+__device__ __forceinline__ float d_round_through(int rt, float v) {
+  if (rt == GT_BF16) return d_bf16_ld(d_bf16_st(v));
+  if (rt == GT_F16) return d_f16_ld(d_f16_st(v));
+  return v;
+}
+
 // storage element -> accumulation type
 template <int DT, class TI, class TA>
 __device__ __forceinline__ TA load_elem(TI x) {

@@ -352,6 +352,7 @@ class Planner {
   void find_patterns();
   bool match_attention(NodeId d2);
   bool match_fp8_epilogue(NodeId castn);
+  bool match_cast_epilogue(NodeId castn);
 
   struct AttnPattern { NodeId q, k, v; float scale; bool causal; };
   struct Fp8Pattern { NodeId dot, xq, wq, sx, sw; };
@@ -364,6 +365,7 @@ class Planner {
   std::vector<bool> absorbed_;
   std::map<NodeId, AttnPattern> attn_pat_;
   std::map<NodeId, Fp8Pattern> fp8_pat_;
+  std::map<NodeId, NodeId> cast_pat_;  // dot -> the cast its GEMM epilogue performs
   std::vector<int> region_step_;
   std::vector<int> slot_producer_;
   std::vector<bool> step_alive_;
@@ -1005,6 +1007,11 @@ void Planner::visit_dot(NodeId id) {
     G.out_dtype = g_.dtype(fp8->second.dot);  // final cast dtype recorded as dot key
     out_dt = G.out_dtype;
   }
+  auto cp = cast_pat_.find(id);
+  if (cp != cast_pat_.end()) {
+    out_dt = G.out_dtype = g_.node(cp->second).op.to;
+    if (n.dtype != DType::F32) G.round_dtype = n.dtype;  // the dot's own rounding, then the cast's
+  }
   int cslot = new_slot(SlotKind::Temp, out_dt, G.batch * G.m * G.n * dt_width(out_dt), id);
   G.c_slot = cslot;
   P_.gemms_.push_back(G);
@@ -1020,6 +1027,7 @@ void Planner::visit_dot(NodeId id) {
   v.view = View::contiguous(n.shape);
   NodeId target = id;
   if (fp8 != fp8_pat_.end()) target = fp8->second.dot;  // the pattern's final node
+  if (cp != cast_pat_.end()) target = cp->second;
   vals_[target] = v;
   if (target != id) vals_[target].view = View::contiguous(g_.shape(target));
 }
@@ -1279,6 +1287,27 @@ bool Planner::match_fp8_epilogue(NodeId castn) {
   return true;
 }
 
+// cast(dot(a, b)) with float dtypes: the GEMM epilogue rounds the f32 accumulator to the dot's
+// dtype and stores it converted to the cast's (graph/ops/core/convert.rs cast of a contraction
+// result, e.g. the matmul-in-f16 policy of graph/pass/amp.rs:16-40 casting back to f32). Taken
+// when the cast narrows or keeps the width (fewer bytes written than the dot's own output) or is
+// itself a result of the plan; a widening cast feeding more elementwise work stays with that
+// region, which reads the narrower dot output instead.
+bool Planner::match_cast_epilogue(NodeId castn) {
+  const Node& cn = g_.node(castn);
+  NodeId dot = cn.src[0];
+  const Node& dn = g_.node(dot);
+  if (dn.op.kind != OpKind::DotGeneral || absorbed_[dot] || fp8_pat_.count(dot) || cast_pat_.count(dot)) return false;
+  if (consumers_[dot] != 1 || root_set_.count(dot)) return false;
+  auto f = [](DType d) { return d == DType::BF16 || d == DType::F16 || d == DType::F32; };
+  const DType d = dn.dtype, t = cn.op.to;
+  if (!f(d) || !f(t) || d == t) return false;
+  if (dt_width(t) > dt_width(d) && !root_set_.count(castn)) return false;
+  absorbed_[castn] = true;
+  cast_pat_[dot] = castn;
+  return true;
+}
+
 void Planner::find_patterns() {
   auto order = reachable_multi(g_, P_.roots_);
   consumers_.assign(g_.size(), 0);
@@ -1290,6 +1319,8 @@ void Planner::find_patterns() {
     if (k == OpKind::DotGeneral && !absorbed_[id]) match_attention(id);
     if (k == OpKind::Cast && !absorbed_[id]) match_fp8_epilogue(id);
   }
+  for (NodeId id : order)
+    if (g_.node(id).op.kind == OpKind::Cast && !absorbed_[id]) match_cast_epilogue(id);
 }
 
 void Planner::visit(NodeId id) {
@@ -1480,6 +1511,7 @@ void Plan::compile() {
       if (G.alpha_slot >= 0) a.alpha = reinterpret_cast<const float*>(16);
       std::ostringstream o;
       o << gemm_variant(a) << " b" << G.batch << " m" << G.m << " n" << G.n << " k" << G.k;
+      if (G.out_dtype != G.in_dtype && G.alpha_slot < 0) o << " +cast " << dt_name(G.out_dtype);
       s.label = o.str();
     } else if (s.type == Step::QUANT) {
       const QuantStep& Q = quants_[s.index];
@@ -1557,6 +1589,7 @@ void Plan::launch_step(const Step& s) {
     a.batch = (int64_t)G.batch; a.m = (int64_t)G.m; a.n = (int64_t)G.n; a.k = (int64_t)G.k;
     a.in_type = (int)G.in_dtype;
     a.out_type = (int)G.out_dtype;
+    a.round_type = G.round_dtype == DType::BF16 || G.round_dtype == DType::F16 ? (int)G.round_dtype : -1;
     if (G.alpha_slot >= 0) a.alpha = static_cast<const float*>(slot_ptr(slots_, G.alpha_slot)) + G.alpha_off;
     if (G.col_scale_slot >= 0) {
       a.col_scale = static_cast<const float*>(slot_ptr(slots_, G.col_scale_slot)) + G.col_scale_off;

@@ -111,10 +111,13 @@ struct GemmStep {
   // fp8 epilogue: C = round(acc * (*alpha) * col_scale[n]); alpha/col_scale from slots
   int alpha_slot = -1, col_scale_slot = -1;
   int64_t alpha_off = 0, col_scale_off = 0, col_scale_stride = 1;
+  // fused cast epilogue: round to round_dtype (the dot's bf16 / f16) before storing out_dtype;
+  // F32 = no extra rounding
+  DType round_dtype = DType::F32;
   std::string variant;
 };
 
-// Weight-only quantized matmul: a fused dequant GEMV (M <= 4), else a dequantize pass into
+// Weight-only quantized matmul: a fused dequant GEMV (M <= 8), else a dequantize pass into
 // `wdq_slot` followed by a GEMM of act x wdq^T.
 struct QuantStep {
   int act_slot = -1, qw_slot = -1, sc_slot = -1, mn_slot = -1, out_slot = -1, wdq_slot = -1;

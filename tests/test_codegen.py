@@ -199,3 +199,40 @@ def test_rope_rejects_bf16_like_the_reference():
     x = g.input([2, 8, 16], DType.BF16)
     with pytest.raises(K.KuError, match="dtype"):
         g.rope(x)
+
+
+def _steps(g, roots):
+    return [l.split(": ", 1)[1] for l in g.codegen(roots).splitlines() if l.startswith("// step ")]
+
+
+@pytest.mark.parametrize("d,t", [(DType.BF16, DType.F32), (DType.F16, DType.F32), (DType.BF16, DType.F16),
+                                 (DType.F32, DType.BF16), (DType.F32, DType.F16)])
+def test_cast_of_a_matmul_rides_in_the_gemm_epilogue(d, t):
+    g = Graph()
+    a = g.input([256, 128], d)
+    b = g.input([128, 512], d)
+    y = g.matmul(a, b)
+    c = g.cast(y, t)
+    steps = _steps(g, [c])
+    assert len(steps) == 1 and steps[0].endswith("+cast " + t.name), steps
+    # the dot itself requested too: the GEMM writes the dot's dtype and a cast kernel follows
+    steps = _steps(g, [y, c])
+    assert len(steps) == 2 and "+cast" not in steps[0], steps
+
+
+def test_widening_cast_feeding_more_work_stays_in_the_region():
+    """cast(f16 dot, f32) -> relu: the elementwise kernel reads the 2-byte dot output and does the
+    cast itself (fusing would write 4 bytes and read them back)."""
+    g = Graph()
+    a = g.input([256, 128], DType.F16)
+    b = g.input([128, 512], DType.F16)
+    r = g.relu(g.cast(g.matmul(a, b), DType.F32))
+    steps = _steps(g, [r])
+    assert len(steps) == 2 and "+cast" not in steps[0], steps
+    # a narrowing cast feeding more work still rides in the GEMM
+    g2 = Graph()
+    a2 = g2.input([256, 128], DType.F32)
+    b2 = g2.input([128, 512], DType.F32)
+    r2 = g2.relu(g2.cast(g2.matmul(a2, b2), DType.BF16))
+    steps = _steps(g2, [r2])
+    assert len(steps) == 2 and steps[0].endswith("+cast BF16"), steps
