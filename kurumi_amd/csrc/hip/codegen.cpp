@@ -454,11 +454,12 @@ void Gen::plan_layout() {
     NC = (int)chunks;
     return;
   }
-  // multi-level programs keep lines in registers: aim at ~8 chunks per thread;
-  // single-level reductions stream: ~16 chunks per thread.
-  // ~16 chunks per thread: long lines get 256-512 threads with the line cached in registers,
-  // which leaves room for two or three groups per CU
-  int target = 16;
+  // ~16 chunks of 16 bytes per thread: long lines get 256-512 threads with the line cached in
+  // registers, which leaves room for two or three groups per CU. Lines of >= 4096 chunks of
+  // 4-byte elements take ~8 (1024 threads): measured on the [8192, 32000] softmax, f32 rows
+  // 5.57-5.60 -> 5.74-5.82 TB/s with 8, while its bf16 rows (8 elements per chunk) lose 3-4 %
+  // with 8 and keep 16.
+  int target = (V == 4 && chunks >= 4096) ? 8 : 16;
   if (const char* e = std::getenv("KURUMI_HIP_LINE_CHUNKS")) target = std::max(1, std::atoi(e));
   uint64_t t = 1;
   while (t < 1024 && t * (uint64_t)target < chunks) t *= 2;
