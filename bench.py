@@ -341,8 +341,9 @@ def bench_copy(hip, steps, warmup):
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 20 warm-up launches bring the clocks up (3 left the bf16 softmax 5-15 % slow on some runs)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--configs", default="1,2,3,4,5,6")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--probe-copy", action="store_true",
@@ -350,7 +351,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"kurumi_hip bench: this run measures one GPU only; --gpus {args.gpus} is not supported "
-              "(every config shards with no exchange step; see DESIGN.md)", file=sys.stderr)
+              "(every config shards with no exchange step)", file=sys.stderr)
         return 2
     K = _ku()
     hip = K.HipBackend()
@@ -358,15 +359,6 @@ def main() -> int:
     head = bench_cfg2(hip, args.steps, args.warmup, "f32")
     g, x, y, a, xt = head.pop("_graph")
     extra = {}
-    # the same step through the host boundary (ku_eval_many with host feeds -> host results):
-    # PCIe-inclusive rate, reported beside the device-resident value
-    hip.eval_many_with(g, [y, a], {x: xt})
-    t0 = time.perf_counter()
-    for _ in range(2):
-        hip.eval_many_with(g, [y, a], {x: xt})
-    host_ms = (time.perf_counter() - t0) * 1e3 / 2
-    extra["cfg2_host_io"] = {"workload": "cfg 2 f32 via ku_eval_many (host feeds in, host tensors out)",
-                             "ms_per_step": host_ms, "gbs": head["algo_bytes"] / (host_ms * 1e-3) / 1e9}
     if "2" in cfgs:
         b16 = bench_cfg2(hip, args.steps, args.warmup, "bf16")
         b16.pop("_graph")
@@ -385,6 +377,16 @@ def main() -> int:
         extra.update(bench_quant(hip, args.steps, args.warmup))
     if args.probe_copy:
         extra["copy_probe"] = bench_copy(hip, args.steps, args.warmup)
+    # the same step through the host boundary (ku_eval_many with host feeds -> host results):
+    # PCIe-inclusive rate, reported beside the device-resident value (last: the GPU idles while
+    # the host copies, which would cool the clocks for the device-resident configs)
+    hip.eval_many_with(g, [y, a], {x: xt})
+    t0 = time.perf_counter()
+    for _ in range(2):
+        hip.eval_many_with(g, [y, a], {x: xt})
+    host_ms = (time.perf_counter() - t0) * 1e3 / 2
+    extra["cfg2_host_io"] = {"workload": "cfg 2 f32 via ku_eval_many (host feeds in, host tensors out)",
+                             "ms_per_step": host_ms, "gbs": head["algo_bytes"] / (host_ms * 1e-3) / 1e9}
     cpu = None if args.no_cpu else cpu_baseline_cfg2(xt)
     line = {
         "metric": "fused softmax+argmax HBM GB/s (cfg 2, f32 [8192,32000]); GEMM/attn TFLOP/s under configs",
