@@ -455,11 +455,11 @@ void Gen::plan_layout() {
     return;
   }
   // ~16 chunks of 16 bytes per thread: long lines get 256-512 threads with the line cached in
-  // registers, which leaves room for two or three groups per CU. Lines of >= 4096 chunks of
-  // 4-byte elements take ~8 (1024 threads): measured on the [8192, 32000] softmax, f32 rows
-  // 5.57-5.60 -> 5.74-5.82 TB/s with 8, while its bf16 rows (8 elements per chunk) lose 3-4 %
-  // with 8 and keep 16.
-  int target = (V == 4 && chunks >= 4096) ? 8 : 16;
+  // registers, which leaves room for two or three groups per CU. Lines of 4-byte elements take
+  // ~8 (twice the threads), measured: the f32 [8192, 32000] softmax rows 5.57-5.60 -> 5.74-5.82
+  // TB/s (1024 threads per row), the f32 [4096, 4096] fused reduce 5.28 -> 5.61 TB/s (128 per
+  // row); the bf16 softmax rows (8 elements per chunk) lose 3-4 % with 8 and keep 16.
+  int target = V == 4 ? 8 : 16;
   if (const char* e = std::getenv("KURUMI_HIP_LINE_CHUNKS")) target = std::max(1, std::atoi(e));
   uint64_t t = 1;
   while (t < 1024 && t * (uint64_t)target < chunks) t *= 2;
@@ -468,7 +468,9 @@ void Gen::plan_layout() {
   while (t < 1024 && lines * t < ((uint64_t)1 << 18) && chunks >= 4 * t) t *= 2;
   TPL = (int)t;
   NC = (int)((chunks + TPL - 1) / TPL);
-  WG = std::max(TPL, 256);
+  // lines of one wave or less share a 256-thread group; a line of several waves is its own group
+  // (its cross-wave combine, barriers included, then spans the whole group)
+  WG = TPL > 64 ? TPL : 256;
   GPW = WG / TPL;
 }
 
@@ -876,6 +878,7 @@ void Gen::emit_red_finish(int ni, int phase) {
       o << "  { auto ov = shx(acc" << r << ", " << m << "); " << comb("ov") << " }\n";
   }
   if (TPL > 64) {
+    if (GPW != 1) throw Error("codegen: a multi-wave line must be its own work-group");
     int W = TPL / 64;
     std::string tag = std::to_string(phase) + "_" + r;
     if (arg) {

@@ -236,3 +236,22 @@ def test_widening_cast_feeding_more_work_stays_in_the_region():
     r2 = g2.relu(g2.cast(g2.matmul(a2, b2), DType.BF16))
     steps = _steps(g2, [r2])
     assert len(steps) == 2 and steps[0].endswith("+cast BF16"), steps
+
+
+@pytest.mark.parametrize("rows,cols,dt", [(4096, 4096, DType.F32), (8192, 4096, DType.F32), (64, 32000, DType.F32),
+                                          (8192, 32000, DType.BF16), (300, 1000, DType.F32)])
+def test_multi_wave_lines_are_one_group_each(rows, cols, dt):
+    """A line spread over several waves folds across them through LDS with a barrier: the group
+    must hold exactly that line (a second line in the group would read the first line's partials)."""
+    import re
+    g = Graph()
+    x = g.input([rows, cols], dt)
+    y = g.sum(g.mul(x, x), 1)
+    src = g.codegen([y])
+    lb = int(re.search(r"__launch_bounds__\((\d+)\)", src).group(1))
+    m = re.search(r"const u32 lane = threadIdx.x % (\d+)u;", src)
+    tpl = int(m.group(1))
+    if tpl > 64:
+        assert lb == tpl, (lb, tpl)
+    else:
+        assert lb % tpl == 0
