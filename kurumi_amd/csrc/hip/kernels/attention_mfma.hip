@@ -122,7 +122,9 @@ attn_mfma_k(AttnArgs a) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[4 * TBYTES];
   KU_LDS unsigned char* lds = (KU_LDS unsigned char*)lds_raw;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, h = lane >> 5, qc = lane & 31;
+  // the wave index is uniform: kept in an SGPR, so the DMA destinations (M0) need no VALU work
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5,
+            qc = lane & 31;
   const int64_t S = a.s;
   const int nqt = (int)((S + BQ - 1) / BQ);
   // heaviest causal tiles first; tile ids with equal head stay on one XCD (bh % 8 == 0 case)
@@ -211,15 +213,13 @@ attn_mfma_k(AttnArgs a) {
   dma(K, 1, kbuf(1), false);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  f32x16 sc[QT][2];
-  s_mfma(kbuf(0), sc);
-
-  for (int kb = 0; kb < nkb; ++kb) {
+  // One block: softmax of sc (this block's S^T) and S^T of the next block into sn. The loop runs
+  // two blocks per trip with the two score sets swapping roles, so no registers are copied.
+  auto block = [&](int kb, f32x16 (&sc)[QT][2], f32x16 (&sn)[QT][2]) __attribute__((always_inline)) {
     // K of block kb+2 and V of block kb+1 into the buffers the previous block freed
     dma(K, kb + 2, kbuf(kb & 1), false);
     dma(V, kb + 1, vbuf((kb + 1) & 1), true);
     const int64_t k0 = (int64_t)kb * BK;
-    f32x16 sn[QT][2];
     u32x4 pf[QT][4];
     if (live) {
 #pragma unroll
@@ -257,6 +257,9 @@ attn_mfma_k(AttnArgs a) {
         }
       }
       // S^T of block kb+1 (its K is already in LDS) interleaved with the exponentials of block kb
+      // wave priority: the section that interleaves the next S^T MFMAs with this block's softmax
+      // goes first when both waves of a SIMD are ready (measured 3 % faster than equal priority)
+      __builtin_amdgcn_s_setprio(1);
       s_mfma(kbuf((kb + 1) & 1), sn);
 #pragma unroll
       for (int u = 0; u < QT; ++u) {
@@ -286,6 +289,7 @@ attn_mfma_k(AttnArgs a) {
       // with ds_read_b64_tr_b16: in each 16-lane group, input lane 4k'+q points at key row k',
       // dims 4q..4q+3, and output lane i receives keys 0..3 of dim i. Two reads fetch exactly the
       // key groups the probability registers hold: 16s + 4h + 0..3 and 16s + 8 + 4h + 0..3.
+      __builtin_amdgcn_s_setprio(0);
       const KU_LDS unsigned char* LV = vbuf(kb & 1);
       const int g = lane >> 4, c16 = lane & 15;
 #pragma unroll
@@ -308,10 +312,12 @@ attn_mfma_k(AttnArgs a) {
     // this thread's DMA for the next blocks has landed; the barrier publishes it
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-#pragma unroll
-    for (int u = 0; u < QT; ++u)
-#pragma unroll
-      for (int t = 0; t < 2; ++t) sc[u][t] = sn[u][t];
+  };
+  f32x16 sa[QT][2], sb[QT][2];
+  s_mfma(kbuf(0), sa);
+  for (int kb = 0; kb < nkb; kb += 2) {
+    block(kb, sa, sb);
+    if (kb + 1 < nkb) block(kb + 1, sb, sa);
   }
 
 #pragma unroll
