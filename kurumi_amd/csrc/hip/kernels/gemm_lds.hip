@@ -410,9 +410,33 @@ void launch_tile(const GemmArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((gemm_lds_k<E, BNMAJ, OT, BM, BN, WM, WN, false>), grid, dim3(WM * WN * 64), 0, s, a);
 }
 
+int cu_count() {
+  static const int n = [] {
+    int dev = 0, c = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+      c = 256;
+    return c;
+  }();
+  return n;
+}
+
+// One work-group per CU at a time (the stages fill the LDS), so the tiles run in rounds of
+// cu_count(). 192-row tiles win when they need no more rounds than 256-row ones by enough to
+// outweigh their ~10 % lower efficiency (a 96 x 64 wave tile reads more LDS per MFMA): measured
+// on the e4m3 [2048, 4096] x [11008, 4096]^T linear, 344 tiles of 256 x 256 (2 rounds, the second
+// a third full) 101 us vs 473 tiles of 192 x 256 (2 full rounds) 90 us; the bf16
+// [4096, 4096] x [4096, 11008] GEMM keeps 256 rows (359 vs 379 us).
+bool rows192(const GemmArgs& a) {
+  const int64_t ncu = cu_count(), tn = (a.n + 255) / 256;
+  const int64_t r256 = ((a.m + 255) / 256 * tn * a.batch + ncu - 1) / ncu;
+  const int64_t r192 = ((a.m + 191) / 192 * tn * a.batch + ncu - 1) / ncu;
+  return (double)r192 * 192 * 1.1 < (double)r256 * 256;
+}
+
 template <int E, bool BNMAJ, int OT>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
-  launch_tile<E, BNMAJ, OT, 256, 256, 2, 4>(a, s);
+  if (rows192(a)) launch_tile<E, BNMAJ, OT, 192, 256, 2, 4>(a, s);
+  else launch_tile<E, BNMAJ, OT, 256, 256, 2, 4>(a, s);
 }
 
 template <int E, bool BNMAJ>
