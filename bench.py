@@ -298,30 +298,37 @@ def bench_nn(hip, steps, warmup):
 
 
 def bench_quant(hip, steps, warmup):
-    """Weight-only int4 decode GEMV (QuantMatmul, M = 1): one token through a [11008, 4096] int4
-    projection (symmetric, group 128, bf16 activations) per layer, 12 layers' weights per plan
-    (12 x 23 MB exceeds the 256 MB last-level cache). HBM-bound on the packed weights + scales."""
+    """Weight-only int4 QuantMatmul through a [11008, 4096] int4 projection (symmetric, group 128,
+    bf16 activations) per layer, 12 layers' weights per plan (12 x 23 MB exceeds the 256 MB
+    last-level cache): one token (M = 1, the fused dequant GEMV) and a batch of 32 tokens (the
+    fused dequant MFMA kernel). Both HBM-bound on the packed weights + scales."""
     K = _ku()
     n, k, grp, layers = 11008, 4096, 128, 12
     rng = np.random.default_rng(0)
-    g = K.Graph()
-    x = g.input([1, k], K.DType.BF16)
-    roots = []
-    for li in range(layers):
+    weights = []
+    for _ in range(layers):
         w = rng.standard_normal((n, k), dtype=np.float32)
         packed, scales, _ = K.quantize(w, 4, grp, True)
-        qw = g.constant_bytes(K.DType.U8, packed.tobytes(), packed.shape)
-        sc = g.constant_bytes(K.DType.F16, scales.tobytes(), scales.shape)
-        roots.append(g.quant_matmul(x, qw, sc, None, 4, grp))
-    xt = device_values(hip, scaled_randn(1.0), [1, k], 601, K.DType.BF16)
-    plan = hip.plan(g, roots, {x: xt})
-    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
-    kms = sum(per_step) / layers
-    algo = n * k // 2 + n * (k // grp) * 2 + k * 2 + n * 2  # packed weight, scales, act, out
-    return {"nn_quant_gemv": {"workload": f"int4 (sym, group {grp}) decode GEMV [1,{k}] x [{n},{k}]^T bf16, "
-                              f"{layers} layers' weights per plan", "ms_per_step": wall_ms / layers,
-                              "kernels": labels[:1], "kernel_ms": per_step[:1], "algo_bytes": algo,
-                              "roofline": roofline_hbm(algo, kms)}}
+        weights.append((packed, scales))
+    out = {}
+    for m, key, what in ((1, "nn_quant_gemv", "decode GEMV"), (32, "nn_quant_mfma", "batched decode (fused MFMA)")):
+        g = K.Graph()
+        x = g.input([m, k], K.DType.BF16)
+        roots = []
+        for packed, scales in weights:
+            qw = g.constant_bytes(K.DType.U8, packed.tobytes(), packed.shape)
+            sc = g.constant_bytes(K.DType.F16, scales.tobytes(), scales.shape)
+            roots.append(g.quant_matmul(x, qw, sc, None, 4, grp))
+        xt = device_values(hip, scaled_randn(1.0), [m, k], 601, K.DType.BF16)
+        plan = hip.plan(g, roots, {x: xt})
+        wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+        kms = sum(per_step) / layers
+        algo = n * k // 2 + n * (k // grp) * 2 + m * k * 2 + m * n * 2  # packed weight, scales, act, out
+        out[key] = {"workload": f"int4 (sym, group {grp}) {what} [{m},{k}] x [{n},{k}]^T bf16, "
+                               f"{layers} layers' weights per plan", "ms_per_step": wall_ms / layers,
+                    "kernels": labels[:1], "kernel_ms": per_step[:1], "algo_bytes": algo,
+                    "roofline": roofline_hbm(algo, kms)}
+    return out
 
 
 def bench_copy(hip, steps, warmup):

@@ -63,5 +63,8 @@ struct QuantArgs {
 bool quant_gemv_ok(const QuantArgs& a);
 void launch_quant_gemv(const QuantArgs& a, hipStream_t s);
 void launch_quant_dequant(const QuantArgs& a, hipStream_t s);
+// fused dequant MFMA kernel: int4, bf16 / f16 act, 9 <= M <= 64, group a multiple of 64
+bool quant_mm_ok(const QuantArgs& a);
+void launch_quant_mm(const QuantArgs& a, hipStream_t s);
 
 }  // namespace ku::hipbk

@@ -323,8 +323,7 @@ __global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
           for (int p = 0; p < H; ++p) {
             // (MAGICV + u) as a 16-bit pair: C ^ (t & PMASK) with C = MAGIC | XOR in one v_bitop3
             // (0x6c: S1 ^ (S0 & S2)); the symmetric offset's xor rides along
-            uint32_t x;
-            asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x6c" : "=v"(x) : "v"(word >> (BITS * p)), "v"(MAGIC | (XOR & PMASK)), "v"(PMASK));
+            const uint32_t x = __builtin_amdgcn_bitop3_b32(word >> (BITS * p), MAGIC | (XOR & PMASK), PMASK, 0x6c);
 #pragma unroll
             for (int m = 0; m < MB; ++m) part[r][m] = dot2<AT>(x, ap[m][p], part[r][m]);
           }
@@ -395,6 +394,186 @@ __global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
     const int64_t n = row0 + r;
     if (n < N && m < a.m) act_st<AT>(a.out, m * N + n, v);
   }
+}
+
+// Fused dequant MFMA kernel (int4, bf16 / f16 act, 9 <= M <= 64: batched decode). Transposed
+// like the attention kernel, C^T[n][m] = W[n][:] . act[m][:] with v_mfma_f32_32x32x16: the A
+// operand is a 32-row tile of the weight, each lane converting the 8 fields of one packed word
+// into 16-bit pairs (MAGICV + u) with v_bitop3 (pairs (p, p + 4) of the word), the B operand the
+// act values of that word in the same order (v_perm), so no LDS staging is needed for either.
+// Lane l owns act row m = l % 32 of each accumulator, which makes the act sum of the magic /
+// offset correction a per-lane value. Per scale group the MFMA partial is folded as
+//   acc += s[n][g] * (C_g - (MAGICV + off) * sum_k act) (+ min[n][g] * sum_k act).
+// Every 64-value block of a row: lane half h reads bytes 16h..16h+15 (words 4h..4h+3) and k-step
+// j of the MFMA takes word 4h + j in half h (a permutation of k shared by both operands). A
+// work-group holds 32 * NT weight rows; its QMM_NW waves take the scale groups round-robin and
+// add their partials through LDS at the end. The rows' scales (and mins) are staged in LDS
+// transposed to [group][row] first.
+constexpr int QMM_NW = 8;
+template <bool SYM, int AT, int NT, int MT>
+__global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  constexpr uint32_t PMASK = 0x000F000Fu;
+  constexpr uint32_t MAGIC = AT == GT_BF16 ? 0x43004300u : 0x64006400u;
+  constexpr float MAGICV = AT == GT_BF16 ? 128.f : 1024.f;
+  constexpr uint32_t CX = MAGIC | (SYM ? 0x00080008u : 0u);  // bitop3 constant: magic + symmetric offset xor
+  constexpr float OFF = SYM ? 8.f : 0.f;
+  constexpr uint32_t ONES = AT == GT_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  constexpr int RW = 32 * NT;  // weight rows per work-group
+  extern __shared__ __attribute__((aligned(16))) unsigned char qmm_lds[];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t K = a.k, N = a.n, M = a.m, rb = K / 2, ng = K / a.group;
+  const int64_t n0 = (int64_t)blockIdx.x * RW;
+  uint16_t* ssc = reinterpret_cast<uint16_t*>(qmm_lds);  // [ng][RW]
+  uint16_t* smn = ssc + ng * RW;
+  for (int64_t i = tid; i < ng * RW; i += QMM_NW * 64) {
+    const int64_t r = i / ng, g = i % ng;  // consecutive threads read along a row of the table
+    const int64_t n = n0 + r < N ? n0 + r : N - 1;
+    ssc[g * RW + r] = a.scales[n * ng + g];
+    if constexpr (!SYM) smn[g * RW + r] = a.mins[n * ng + g];
+  }
+  __syncthreads();
+
+  const uint8_t* wrow[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int64_t n = n0 + 32 * t + l32;
+    wrow[t] = a.qw + (n < N ? n : N - 1) * rb + 16 * h;
+  }
+  const uint16_t* arow[MT];
+  bool alive[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int64_t m = 32 * mt + l32;
+    alive[mt] = m < M;
+    arow[mt] = static_cast<const uint16_t*>(a.act) + (m < M ? m : 0) * K + 32 * h;
+  }
+  f32x16 acc[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[t][mt][v] = 0.f;
+  const int bpg = (int)(a.group / 64);  // 64-value blocks per group
+  for (int64_t g = wave; g < ng; g += QMM_NW) {
+    f32x16 cg[NT][MT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) cg[t][mt][v] = 0.f;
+    float as[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) as[mt] = 0.f;
+    for (int b = 0; b < bpg; ++b) {
+      const int64_t kb = g * a.group + 64 * b;  // first k of the block
+      u32x4 w[NT];
+#pragma unroll
+      for (int t = 0; t < NT; ++t) w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[t] + kb / 2));
+      uint32_t aw[MT][16];  // act values kb + 32h .. +31 of this lane's row
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const u32x4 v = alive[mt] ? *reinterpret_cast<const u32x4*>(arow[mt] + kb + 8 * q) : u32x4{0, 0, 0, 0};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            aw[mt][4 * q + i] = v[i];
+            as[mt] = dot2<AT>(v[i], ONES, as[mt]);
+          }
+        }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // k-step j: word 4h + j of each row; act pairs (p, p + 4) of the same 8 values
+        u32x4 bf[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            constexpr uint32_t SEL[2] = {0x05040100u, 0x07060302u};
+            bf[mt][p] = __builtin_amdgcn_perm(aw[mt][4 * j + ((p + 4) >> 1)], aw[mt][4 * j + (p >> 1)], SEL[p & 1]);
+          }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          u32x4 af;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            // through the builtin, not inline asm: the compiler then keeps the wait states a VALU
+            // result needs before an MFMA reads it
+            af[p] = __builtin_amdgcn_bitop3_b32(w[t][j] >> (4 * p), CX, PMASK, 0x6c);
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            if constexpr (AT == GT_BF16)
+              cg[t][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af),
+                                                                  __builtin_bit_cast(bf16x8, bf[mt]), cg[t][mt], 0, 0, 0);
+            else
+              cg[t][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, af),
+                                                                 __builtin_bit_cast(f16x8, bf[mt]), cg[t][mt], 0, 0, 0);
+          }
+        }
+      }
+    }
+    // the group's act sum of this lane's row: both lane halves
+    float at[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(as[mt]), __float_as_uint(as[mt]), false, false);
+      at[mt] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);  // C row = weight row of the tile
+        const float sc = f16_to_f32(ssc[g * RW + r]);
+        const float mn = SYM ? 0.f : f16_to_f32(smn[g * RW + r]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[t][mt][v] = fmaf(sc, fmaf(-(MAGICV + OFF), at[mt], cg[t][mt][v]), acc[t][mt][v]);
+          if constexpr (!SYM) acc[t][mt][v] = fmaf(mn, at[mt], acc[t][mt][v]);
+        }
+      }
+  }
+  // partials of the waves through LDS (the scale table is no longer read)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(qmm_lds);  // [wave][t][mt][v][lane]
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) red[(((wave * NT + t) * MT + mt) * 16 + v) * 64 + lane] = acc[t][mt][v];
+  __syncthreads();
+  constexpr int PER = NT * MT * 16 * 64;  // elements of one wave's partial
+  for (int e = tid; e < PER; e += QMM_NW * 64) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < QMM_NW; ++w) sum += red[w * PER + e];
+    const int ln = e & 63, v = (e >> 6) & 15, mt = (e >> 10) % MT, t = (e >> 10) / MT;
+    const int64_t m = 32 * mt + (ln & 31);
+    const int64_t n = n0 + 32 * t + 8 * (v >> 2) + 4 * (ln >> 5) + (v & 3);
+    if (m < M && n < N) act_st<AT>(a.out, m * N + n, sum);
+  }
+}
+
+template <bool SYM, int AT, int NT, int MT>
+void launch_mm(const QuantArgs& a, hipStream_t s) {
+  const int64_t ng = a.k / a.group;
+  const size_t lds = std::max<size_t>((size_t)ng * 32 * NT * 2 * (SYM ? 1 : 2), (size_t)QMM_NW * NT * MT * 16 * 64 * 4);
+  const dim3 grid((unsigned)((a.n + 32 * NT - 1) / (32 * NT)));
+  hipLaunchKernelGGL((quant_mm_k<SYM, AT, NT, MT>), grid, dim3(QMM_NW * 64), lds, s, a);
+}
+
+template <bool SYM, int AT>
+void mm_at(const QuantArgs& a, hipStream_t s) {
+  if (a.m <= 32) launch_mm<SYM, AT, 2, 1>(a, s);
+  else launch_mm<SYM, AT, 1, 2>(a, s);
 }
 
 // one thread per packed byte of the weight: its 8/BITS values into wdq [N, K] (dtype WT)
@@ -490,6 +669,33 @@ void launch_quant_gemv(const QuantArgs& a, hipStream_t s) {
     case 8: gemv_bits<4, false>(a, s); return;
     case 17: gemv_bits<8, true>(a, s); return;
     default: gemv_bits<8, false>(a, s); return;
+  }
+}
+
+// LDS bytes of the fused MFMA kernel: the staged scale (and min) table, or the wave partials
+static size_t quant_mm_lds(const QuantArgs& a) {
+  const int nt = a.m <= 32 ? 2 : 1, mt = a.m <= 32 ? 1 : 2;
+  return std::max<size_t>((size_t)(a.k / a.group) * 32 * nt * 2 * (a.sym ? 1 : 2), (size_t)QMM_NW * nt * mt * 16 * 64 * 4);
+}
+
+bool quant_mm_ok(const QuantArgs& a) {
+  return a.bits == 4 && (a.act_type == GT_BF16 || a.act_type == GT_F16) && a.m > 8 && a.m <= 64 && a.group > 0 &&
+         a.group % 64 == 0 && a.k % a.group == 0 && a.k < (int64_t(1) << 31) && quant_mm_lds(a) <= 160 * 1024 &&
+         (a.sym || a.mins);
+}
+
+void launch_quant_mm(const QuantArgs& a, hipStream_t s) {
+  check(a);
+  if (!quant_mm_ok(a)) throw std::runtime_error("quant: shape not supported by the fused MFMA kernel");
+  if (a.n == 0) return;
+  if ((reinterpret_cast<uintptr_t>(a.qw) & 15) || (reinterpret_cast<uintptr_t>(a.act) & 15))
+    throw std::runtime_error("quant: packed weight and act must be 16-byte aligned");
+  if (a.sym) {
+    if (a.act_type == GT_BF16) mm_at<true, GT_BF16>(a, s);
+    else mm_at<true, GT_F16>(a, s);
+  } else {
+    if (a.act_type == GT_BF16) mm_at<false, GT_BF16>(a, s);
+    else mm_at<false, GT_F16>(a, s);
   }
 }
 

@@ -1059,8 +1059,15 @@ void Planner::visit_quant(NodeId id) {
   Q.act_dtype = at;
   Q.wdq_dtype = at;  // bf16 / f16 act: the MFMA GEMM on rounded weights; f32: the generic GEMM
   Q.out_slot = new_slot(SlotKind::Temp, at, Q.m * Q.n * dt_width(at), id);
-  // M <= 8: the fused dequant GEMV (quant_gemv_ok); above: dequantise once + GEMM
-  if (!(Q.m >= 1 && Q.m <= 8)) Q.wdq_slot = new_slot(SlotKind::Temp, Q.wdq_dtype, Q.n * Q.k * dt_width(Q.wdq_dtype), id);
+  // M <= 8: the fused dequant GEMV; int4 with 9 <= M <= 64 (bf16 / f16 act): the fused dequant
+  // MFMA kernel; otherwise dequantise once into wdq, then the GEMM
+  QuantArgs qa;
+  qa.m = (int64_t)Q.m; qa.n = (int64_t)Q.n; qa.k = (int64_t)Q.k; qa.group = (int64_t)Q.group;
+  qa.bits = Q.bits; qa.sym = Q.sym; qa.act_type = (int)at;
+  qa.mins = Q.sym ? nullptr : reinterpret_cast<const uint16_t*>(16);  // shape check only
+  Q.path = quant_gemv_ok(qa) ? QuantStep::GEMV : (quant_mm_ok(qa) ? QuantStep::MFMA : QuantStep::DEQUANT_GEMM);
+  if (Q.path == QuantStep::DEQUANT_GEMM)
+    Q.wdq_slot = new_slot(SlotKind::Temp, Q.wdq_dtype, Q.n * Q.k * dt_width(Q.wdq_dtype), id);
   P_.quants_.push_back(Q);
   int step = new_step(Step::QUANT, (int)P_.quants_.size() - 1, "quant");
   for (int i = 0; i < 4; ++i)
@@ -1516,7 +1523,8 @@ void Plan::compile() {
     } else if (s.type == Step::QUANT) {
       const QuantStep& Q = quants_[s.index];
       std::ostringstream o;
-      o << (Q.wdq_slot < 0 ? "quant_gemv" : "quant_dequant+gemm") << " int" << Q.bits << (Q.sym ? "s" : "a") << " g"
+      o << (Q.path == QuantStep::GEMV ? "quant_gemv" : Q.path == QuantStep::MFMA ? "quant_mfma" : "quant_dequant+gemm")
+        << " int" << Q.bits << (Q.sym ? "s" : "a") << " g"
         << Q.group << " m" << Q.m << " n" << Q.n << " k" << Q.k;
       s.label = o.str();
     } else {
@@ -1616,8 +1624,10 @@ void Plan::launch_step(const Step& s) {
     a.bits = Q.bits; a.sym = Q.sym;
     a.act_type = (int)Q.act_dtype; a.wdq_type = (int)Q.wdq_dtype;
     if (Q.m * Q.n == 0) return;
-    if (Q.wdq_slot < 0) {
+    if (Q.path == QuantStep::GEMV) {
       launch_quant_gemv(a, st);
+    } else if (Q.path == QuantStep::MFMA) {
+      launch_quant_mm(a, st);
     } else {
       a.wdq = slot_ptr(slots_, Q.wdq_slot);
       launch_quant_dequant(a, st);

@@ -117,9 +117,11 @@ struct GemmStep {
   std::string variant;
 };
 
-// Weight-only quantized matmul: a fused dequant GEMV (M <= 8), else a dequantize pass into
-// `wdq_slot` followed by a GEMM of act x wdq^T.
+// Weight-only quantized matmul: a fused dequant GEMV (M <= 8), the fused dequant MFMA kernel
+// (int4, 9 <= M <= 64), else a dequantize pass into `wdq_slot` followed by a GEMM of act x wdq^T.
 struct QuantStep {
+  enum Path { GEMV, MFMA, DEQUANT_GEMM };
+  Path path = GEMV;
   int act_slot = -1, qw_slot = -1, sc_slot = -1, mn_slot = -1, out_slot = -1, wdq_slot = -1;
   int64_t act_off = 0, qw_off = 0, sc_off = 0, mn_off = 0;  // elements
   size_t m = 0, n = 0, k = 0, group = 0;

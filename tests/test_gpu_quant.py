@@ -79,3 +79,29 @@ def test_quant_decode_full_size(hip):
     got = to_f32(hip.eval_with(g, y, {x: xt}))
     assert rel_err(got, truth) <= 1e-2
     assert_close(got, truth, rtol=1e-2, atol=1e-2 * np.abs(truth).max(), what="decode")
+
+
+@pytest.mark.parametrize("m", [9, 32, 33, 64])
+@pytest.mark.parametrize("sym", [True, False])
+@pytest.mark.parametrize("act_dt", [DType.BF16, DType.F16])
+@pytest.mark.parametrize("group", [64, 128, 256])
+def test_quant_mfma_path_matches_oracle(hip, m, sym, act_dt, group):
+    """The fused dequant MFMA kernel (int4, 9 <= M <= 64): row counts that cut the 32-row weight
+    tiles (100) and the 32-row act tiles (9, 33), every group size it takes."""
+    print(f"quant mfma m={m} sym={sym} {act_dt.name} g={group}", flush=True)
+    g, x, y, xt, truth = build(m, 100, 512, 4, group, sym, act_dt, 300 + m + group)
+    steps = [l for l in g.codegen([y]).splitlines() if l.startswith("// step ")]
+    assert any("quant_mfma" in st for st in steps), steps
+    got = to_f32(hip.eval_with(g, y, {x: xt}))
+    assert rel_err(got, truth) <= 1e-2, rel_err(got, truth)
+    want = to_f32(interpret(g, [y], {x: xt})[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="quant mfma vs oracle")
+
+
+def test_quant_mfma_batched_decode_size(hip):
+    """A batch of 32 tokens through the int4 (group 128) [11008, 4096] projection."""
+    print("quant mfma 32x4096 -> 11008", flush=True)
+    g, x, y, xt, truth = build(32, 11008, 4096, 4, 128, True, DType.BF16, 12)
+    got = to_f32(hip.eval_with(g, y, {x: xt}))
+    assert rel_err(got, truth) <= 1e-2
+    assert_close(got, truth, rtol=1e-2, atol=1e-2 * np.abs(truth).max(), what="batched decode")

@@ -172,11 +172,25 @@ def test_quant_matmul_record_time_errors():
             f()
 
 
+def test_plan_picks_the_mfma_kernel_for_int4_batches():
+    rng = np.random.default_rng(4)
+    w = rng.standard_normal((64, 256)).astype(np.float32)
+    cases = [(4, 128, DType.BF16, 16, "quant_mfma"), (4, 64, DType.F16, 64, "quant_mfma"),
+             (4, 128, DType.BF16, 65, "quant_dequant+gemm"), (4, 128, DType.F32, 16, "quant_dequant+gemm"),
+             (8, 128, DType.BF16, 16, "quant_dequant+gemm"), (4, 32, DType.BF16, 16, "quant_dequant+gemm")]
+    for bits, group, dt, m, want in cases:
+        p, s, mn = K.quantize(w, bits, group, True)
+        g, y = quant_graph(rng.standard_normal((m, 256)).astype(np.float32), p, s, mn, bits, group, dt)
+        src = g.codegen([y])
+        steps = [l.split(": ", 1)[1] for l in src.splitlines() if l.startswith("// step ")]
+        assert any(st.startswith(want) for st in steps), (bits, group, dt, m, steps)
+
+
 def test_plan_labels_gemv_and_gemm_paths():
     rng = np.random.default_rng(3)
     p, s, mn = K.quantize(rng.standard_normal((64, 128)).astype(np.float32), 4, 32, True)
     for m, want in ((1, "quant_gemv int4s g32 m1 n64 k128"), (4, "quant_gemv"), (8, "quant_gemv"), (9, "quant_dequant+gemm"),
-                    (16, "quant_dequant+gemm")):
+                    (65, "quant_dequant+gemm")):
         g, y = quant_graph(rng.standard_normal((m, 128)).astype(np.float32), p, s, mn, 4, 32, DType.BF16)
         src = g.codegen([y])
         steps = [l.split(": ", 1)[1] for l in src.splitlines() if l.startswith("// step ")]
