@@ -16,6 +16,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstdint>
 #include <stdexcept>
 #include <string>
@@ -410,7 +411,7 @@ __global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
 // add their partials through LDS at the end. The rows' scales (and mins) are staged in LDS
 // transposed to [group][row] first.
 constexpr int QMM_NW = 8;
-template <bool SYM, int AT, int NT, int MT>
+template <bool SYM, int AT, int NT, int MT, int GB>
 __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -458,68 +459,74 @@ __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[t][mt][v] = 0.f;
-  const int bpg = (int)(a.group / 64);  // 64-value blocks per group
-  for (int64_t g = wave; g < ng; g += QMM_NW) {
-    f32x16 cg[NT][MT];
+  // The wave's K range is a contiguous run of sub-groups of GB blocks of 64 values (GB * 64 divides
+  // the scale group, so each sub-group has one scale per row and folds on its own). The loads of
+  // sub-group i + 1 are issued before sub-group i is computed (two register sets that swap roles).
+  const int nsg = (int)(K / (64 * GB));
+  const int spw = (nsg + QMM_NW - 1) / QMM_NW, sbeg = wave * spw, send = min(nsg, sbeg + spw);
+  const int sg_per_group = (int)(a.group / (64 * GB));
+  auto load = [&](int sg, u32x4 (&w)[GB][NT], uint32_t (&aw)[GB][MT][16]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int t = 0; t < NT; ++t)
+    for (int bb = 0; bb < GB; ++bb) {
+      const int kb = (sg * GB + bb) * 64;  // first k of the block
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) cg[t][mt][v] = 0.f;
-    float as[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) as[mt] = 0.f;
-    for (int b = 0; b < bpg; ++b) {
-      const int64_t kb = g * a.group + 64 * b;  // first k of the block
-      u32x4 w[NT];
-#pragma unroll
-      for (int t = 0; t < NT; ++t) w[t] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[t] + kb / 2));
-      uint32_t aw[MT][16];  // act values kb + 32h .. +31 of this lane's row
+      for (int t = 0; t < NT; ++t) w[bb][t] = *reinterpret_cast<const u32x4*>(wrow[t] + kb / 2);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const u32x4 v = alive[mt] ? *reinterpret_cast<const u32x4*>(arow[mt] + kb + 8 * q) : u32x4{0, 0, 0, 0};
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            aw[mt][4 * q + i] = v[i];
-            as[mt] = dot2<AT>(v[i], ONES, as[mt]);
-          }
+          for (int i = 0; i < 4; ++i) aw[bb][mt][4 * q + i] = v[i];
         }
+    }
+  };
+  auto step = [&](int sg, const u32x4 (&w)[GB][NT], const uint32_t (&aw)[GB][MT][16]) __attribute__((always_inline)) {
+    f32x16 cg[NT][MT];
+    float as[MT];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        // k-step j: word 4h + j of each row; act pairs (p, p + 4) of the same 8 values
+    for (int mt = 0; mt < MT; ++mt) {
+      as[mt] = 0.f;
+#pragma unroll
+      for (int bb = 0; bb < GB; ++bb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) as[mt] = dot2<AT>(aw[bb][mt][i], ONES, as[mt]);
+    }
+#pragma unroll
+    for (int bb = 0; bb < GB; ++bb)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        // k-step jj of block bb: word 4h + jj of each row; act pairs (p, p + 4) of the same 8 values
         u32x4 bf[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int p = 0; p < 4; ++p) {
             constexpr uint32_t SEL[2] = {0x05040100u, 0x07060302u};
-            bf[mt][p] = __builtin_amdgcn_perm(aw[mt][4 * j + ((p + 4) >> 1)], aw[mt][4 * j + (p >> 1)], SEL[p & 1]);
+            bf[mt][p] = __builtin_amdgcn_perm(aw[bb][mt][4 * jj + ((p + 4) >> 1)], aw[bb][mt][4 * jj + (p >> 1)], SEL[p & 1]);
           }
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           u32x4 af;
 #pragma unroll
-          for (int p = 0; p < 4; ++p) {
+          for (int p = 0; p < 4; ++p)
             // through the builtin, not inline asm: the compiler then keeps the wait states a VALU
             // result needs before an MFMA reads it
-            af[p] = __builtin_amdgcn_bitop3_b32(w[t][j] >> (4 * p), CX, PMASK, 0x6c);
-          }
+            af[p] = __builtin_amdgcn_bitop3_b32(w[bb][t][jj] >> (4 * p), CX, PMASK, 0x6c);
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
+            const f32x16 c = (bb == 0 && jj == 0) ? f32x16{} : cg[t][mt];  // the sub-group starts from zero
             if constexpr (AT == GT_BF16)
               cg[t][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af),
-                                                                  __builtin_bit_cast(bf16x8, bf[mt]), cg[t][mt], 0, 0, 0);
+                                                                  __builtin_bit_cast(bf16x8, bf[mt]), c, 0, 0, 0);
             else
               cg[t][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, af),
-                                                                 __builtin_bit_cast(f16x8, bf[mt]), cg[t][mt], 0, 0, 0);
+                                                                 __builtin_bit_cast(f16x8, bf[mt]), c, 0, 0, 0);
           }
         }
       }
-    }
-    // the group's act sum of this lane's row: both lane halves
+    // the sub-group's act sum of this lane's row over both lane halves, then the fold
+    const int g = sg / sg_per_group;
     float at[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -539,6 +546,16 @@ __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
           if constexpr (!SYM) acc[t][mt][v] = fmaf(mn, at[mt], acc[t][mt][v]);
         }
       }
+  };
+  u32x4 w0[GB][NT], w1[GB][NT];
+  uint32_t a0[GB][MT][16], a1[GB][MT][16];
+  if (sbeg < send) load(sbeg, w0, a0);
+  for (int sg = sbeg; sg < send; sg += 2) {
+    if (sg + 1 < send) load(sg + 1, w1, a1);
+    step(sg, w0, a0);
+    if (sg + 1 >= send) break;
+    if (sg + 2 < send) load(sg + 2, w0, a0);
+    step(sg + 1, w1, a1);
   }
   // partials of the waves through LDS (the scale table is no longer read)
   __syncthreads();
@@ -567,7 +584,9 @@ void launch_mm(const QuantArgs& a, hipStream_t s) {
   const int64_t ng = a.k / a.group;
   const size_t lds = std::max<size_t>((size_t)ng * 32 * NT * 2 * (SYM ? 1 : 2), (size_t)QMM_NW * NT * MT * 16 * 64 * 4);
   const dim3 grid((unsigned)((a.n + 32 * NT - 1) / (32 * NT)));
-  hipLaunchKernelGGL((quant_mm_k<SYM, AT, NT, MT>), grid, dim3(QMM_NW * 64), lds, s, a);
+  // sub-groups of two 64-value blocks when the scale group allows
+  if (a.group % 128 == 0) hipLaunchKernelGGL((quant_mm_k<SYM, AT, NT, MT, 2>), grid, dim3(QMM_NW * 64), lds, s, a);
+  else hipLaunchKernelGGL((quant_mm_k<SYM, AT, NT, MT, 1>), grid, dim3(QMM_NW * 64), lds, s, a);
 }
 
 template <bool SYM, int AT>
@@ -679,6 +698,7 @@ static size_t quant_mm_lds(const QuantArgs& a) {
 }
 
 bool quant_mm_ok(const QuantArgs& a) {
+  if (const char* e = std::getenv("KURUMI_HIP_NO_MFMA"); e && *e && *e != '0') return false;
   return a.bits == 4 && (a.act_type == GT_BF16 || a.act_type == GT_F16) && a.m > 8 && a.m <= 64 && a.group > 0 &&
          a.group % 64 == 0 && a.k % a.group == 0 && a.k < (int64_t(1) << 31) && quant_mm_lds(a) <= 160 * 1024 &&
          (a.sym || a.mins);
