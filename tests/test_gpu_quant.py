@@ -105,3 +105,17 @@ def test_quant_mfma_batched_decode_size(hip):
     got = to_f32(hip.eval_with(g, y, {x: xt}))
     assert rel_err(got, truth) <= 1e-2
     assert_close(got, truth, rtol=1e-2, atol=1e-2 * np.abs(truth).max(), what="batched decode")
+
+
+@pytest.mark.parametrize("m,k,group,sym,act_dt", [(33, 2048, 64, False, DType.F16), (20, 4096, 256, True, DType.BF16),
+                                                  (64, 1024, 128, False, DType.BF16)])
+def test_quant_mfma_long_k_matches_oracle(hip, m, k, group, sym, act_dt):
+    """Longer K: every wave of the MFMA kernel takes several sub-groups (the one-ahead prefetch
+    runs), groups of 64 (one block per sub-group) and 256 (two sub-groups per scale)."""
+    print(f"quant mfma long k m={m} k={k} g={group} sym={sym} {act_dt.name}", flush=True)
+    g, x, y, xt, truth = build(m, 100, k, 4, group, sym, act_dt, 500 + m + k)
+    got = to_f32(hip.eval_with(g, y, {x: xt}))
+    assert rel_err(got, truth) <= 1e-2, rel_err(got, truth)
+    if m * k <= 33 * 2048:
+        want = to_f32(interpret(g, [y], {x: xt})[0])
+        assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="long-K quant mfma vs oracle")
