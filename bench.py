@@ -1,4 +1,4 @@
-"""kurumi_hip benchmark: the five BASELINE configs on one MI355X, plus the CPU baseline.
+"""kurumi_hip benchmark: the five headline configs on one MI355X, plus the CPU baseline.
 
 The headline line (metric/value) is config 2 — row softmax over [8192, 32000] f32 built from
 primitives (reduce_max, sub, exp, sum, div) followed by argmax -> int32 — as HBM GB/s of the

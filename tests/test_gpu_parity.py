@@ -1,6 +1,6 @@
 """Device-vs-oracle parity of the five hot-path configs and the primitives under them.
 
-Bars: integer, bool and index outputs bit-exact; f32 <= 1e-5 relative;
+Bars (the hot path's stated tolerances): integer, bool and index outputs bit-exact; f32 <= 1e-5 relative;
 bf16/f16 <= 1e-2 relative; fp8 GEMM <= 3e-2 relative against the dequantised-f64 product.
 Floating tolerances are normwise (max|err| / max|ref|) plus an elementwise bound with an
 absolute floor of the same relative size, so cancellation near zero does not hide as noise.
