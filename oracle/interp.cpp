@@ -362,6 +362,9 @@ Tensor reduce(const Op& op, const Tensor& a) {
   AxisIter it = axis_iter(a.shape, axis);
   DType dt = a.dtype;
   if (op.kind == OpKind::ArgReduce) {  // arg_reduce_t: strict compare, first index wins
+    // interp/reduce.rs:46 reads element 0 of the axis before the loop: an empty axis with a
+    // non-empty output is out of bounds there (a panic); here an error
+    if (it.len == 0 && it.outer * it.inner > 0) throw std::runtime_error("arg_reduce over an empty axis");
     Tensor o = make(DType::I64, os);
     int64_t* r = reinterpret_cast<int64_t*>(o.bytes.data());
     bool mn = op.arg == ku::ArgKind::Min;

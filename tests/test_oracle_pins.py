@@ -354,3 +354,17 @@ def test_realize_cfg1_is_two_passes():
     got, passes = realize(g, y, feeds)
     assert passes == 2
     np.testing.assert_array_equal(got.numpy(), np.full(8, 64.0, np.float32))
+
+
+def test_arg_reduce_over_an_empty_axis_is_an_error():
+    """interp/reduce.rs:46 reads element 0 of the reduced axis first; with an empty axis and a
+    non-empty output that is out of bounds (the reference panics): the oracle raises."""
+    g = Graph()
+    x = g.input([3, 0], DType.F32)
+    y = g.argmax(x, 1)
+    with pytest.raises(RuntimeError, match="empty axis"):
+        interpret(g, [y], {x: Tensor.from_numpy(np.zeros((3, 0), np.float32))})
+    # sum / max over an empty axis give the identities, like the reference's folds
+    s = interpret(g, [g.sum(x, 1), g.reduce_max(x, 1)], {x: Tensor.from_numpy(np.zeros((3, 0), np.float32))})
+    np.testing.assert_array_equal(s[0].numpy(), [0, 0, 0])
+    np.testing.assert_array_equal(s[1].numpy(), [-np.inf] * 3)
