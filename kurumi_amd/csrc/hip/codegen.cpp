@@ -417,7 +417,11 @@ void Gen::plan_layout() {
   if (!flat)
     for (int d = a + 1; d < rank; ++d) inner *= R.S[d];
   L = flat ? R.S[rank - 1] : R.S[a];
-  lines = flat ? N / std::max<uint64_t>(L, 1) : N / std::max<uint64_t>(L, 1);
+  // lines: the iteration shape without its line axis (still counted when that axis is empty: a
+  // reduction over a zero-length axis writes its identity to every line)
+  lines = 1;
+  for (int d = 0; d < rank; ++d)
+    if (d != (flat ? rank - 1 : a)) lines *= R.S[d];
   // vector width: 16 bytes of the narrowest streamed type, only along a contiguous last axis
   int minw = 8;
   bool contiguous_axis = flat || inner == 1;

@@ -1389,7 +1389,10 @@ void Planner::visit(NodeId id) {
       return;
     }
     case OpKind::Sum: case OpKind::Prod: case OpKind::ReduceMax: case OpKind::ArgReduce:
-      if (numel(g_.shape(n.src[0])) == 0) throw Error("kurumi_hip: reduction over an empty tensor");
+      // interp/reduce.rs:46 reads element 0 of the axis first: argmax / argmin over an empty
+      // axis (with a non-empty result) is an error there too; sum / prod / max fold to identities
+      if (n.op.kind == OpKind::ArgReduce && numel(g_.shape(n.src[0])) == 0 && numel(n.shape) > 0)
+        throw Error("kurumi_hip: arg_reduce over an empty axis");
       visit_reduce(id);
       return;
     case OpKind::Softmax: case OpKind::RmsNorm:

@@ -9,7 +9,7 @@ Mirrors the reference's `*_matches_cpu` device tests (kurumi_metal/src/tests/*.r
 import numpy as np
 import pytest
 
-from kurumi_amd import DType, Graph, Tensor
+from kurumi_amd import DType, Graph, KuError, Tensor
 from kutest import (assert_close, bf16_bits_to_f32, cast_bits, f32_to_bf16_bits, interpret, rand_range, randn,
                     rel_err, to_f32)
 
@@ -409,3 +409,42 @@ def test_half_casts_bit_exact_for_every_pattern(hip, frm, to):
     got = hip.eval_with(g, c, {x: Tensor(frm, [bits.size], bits.tobytes())}).numpy()
     want = cast_bits(bits, frm, to)
     np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+# ---------------- empty shapes ----------------
+
+@pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
+def test_reductions_over_an_empty_axis_give_the_identity(hip, dt):
+    """interp/reduce.rs:67-83 folds from the identity (sum 0, prod 1, max -inf), so an empty
+    axis yields it on every line; an empty result stays empty."""
+    print(f"empty reductions {dt.name}", flush=True)
+    g = Graph()
+    x = g.input([3, 0], dt)
+    z = g.input([2, 0, 5], dt)
+    e = g.input([0, 8], dt)
+    outs = [g.sum(x, 1), g.prod(x, 1), g.reduce_max(x, 1), g.sum(z, 1), g.reduce_max(z, 1), g.sum(e, 1), g.add(x, x)]
+    mk = (lambda s: Tensor(dt, s, b"")) if dt != DType.F32 else (lambda s: Tensor.from_numpy(np.zeros(s, np.float32)))
+    feeds = {x: mk((3, 0)), z: mk((2, 0, 5)), e: mk((0, 8))}
+    got = hip.eval_many_with(g, outs, feeds)
+    want = interpret(g, outs, feeds)
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert a.shape == b.shape and a.dtype == b.dtype, (i, a.shape, b.shape)
+        np.testing.assert_array_equal(a.numpy(), b.numpy(), err_msg=f"output {i}")
+
+
+def test_matmul_with_an_empty_contraction_is_zero(hip):
+    g = Graph()
+    a = g.input([3, 0], DType.F32)
+    b = g.input([0, 5], DType.F32)
+    y = g.matmul(a, b)
+    got = hip.eval_with(g, y, {a: Tensor.from_numpy(np.zeros((3, 0), np.float32)),
+                               b: Tensor.from_numpy(np.zeros((0, 5), np.float32))}).numpy()
+    np.testing.assert_array_equal(got, np.zeros((3, 5), np.float32))
+
+
+def test_argmax_over_an_empty_axis_is_an_error(hip):
+    """interp/reduce.rs:46 reads element 0 of the axis first (a panic on an empty one)."""
+    g = Graph()
+    x = g.input([3, 0], DType.F32)
+    with pytest.raises(KuError, match="empty axis"):
+        hip.eval_with(g, g.argmax(x, 1), {x: Tensor.from_numpy(np.zeros((3, 0), np.float32))})
