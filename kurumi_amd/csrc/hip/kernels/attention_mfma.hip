@@ -92,15 +92,12 @@ __device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 // the result is the same softmax (numerator and denominator share the stale max).
 constexpr float RESCALE = 8.f;
 
-// Scheduling hints (llvm.amdgcn.sched.group.barrier masks): interleave the MFMAs of one product
-// with the VALU work of the softmax, so the matrix core and the vector ALU run side by side.
-constexpr int SG_VALU = 0x2, SG_MFMA = 0x8, SG_DSR = 0x100, SG_DSW = 0x200;
 
 // QT 32-query tiles per wave: QT = 2 halves the LDS bytes per MFMA (every K / V fragment feeds
 // two MFMAs) at the price of one wave per SIMD.
 //
-// Software pipeline per block kb (one barrier each): the S^T MFMAs of block kb+1 are issued
-// between the softmax instructions of block kb; then the P.V MFMAs of block kb run while the
+// Software pipeline per block kb (one barrier each): the S^T MFMAs of block kb+1 are independent
+// of the softmax instructions of block kb, so the two interleave; then the P.V MFMAs of block kb run while the
 // staged K of block kb+2 and V of block kb+1 are written to LDS. K and V have separate
 // double buffers, K one block ahead of V.
 template <int D, int DT, int NW, int QT>
@@ -278,12 +275,6 @@ attn_mfma_k(AttnArgs a) {
             pf[u][2 * t + (v2 >> 2)][v2 & 3] = pp;
           }
         l[u] += rs[0] + rs[1];
-      }
-#pragma unroll
-      for (int i = 0; i < DS * 2; ++i) {
-        __builtin_amdgcn_sched_group_barrier(SG_DSR, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_MFMA, QT, 0);
-        __builtin_amdgcn_sched_group_barrier(SG_VALU, 96 * QT / (DS * 2), 0);
       }
       // O^T += V^T . P^T for block kb. V^T fragments come straight from the row-major V block
       // with ds_read_b64_tr_b16: in each 16-lane group, input lane 4k'+q points at key row k',
