@@ -461,10 +461,14 @@ void Gen::plan_layout() {
   // Chunks of 16 bytes per thread, the line cached in registers. Lines of 4-byte elements take ~8
   // per thread, measured: the f32 [8192, 32000] softmax rows 5.57-5.60 -> 5.74-5.82 TB/s (1024
   // threads per row, from 16 chunks), the f32 [4096, 4096] fused reduce 5.28 -> 5.61 TB/s (128
-  // per row). Lines of 2-byte elements take 256 threads: the bf16 softmax rows (16 chunks each)
+  // per row); when a full-size output is stored too, ~2 (up to 1024 threads): the f32
+  // [8192, 4096] rmsnorm 5.76 -> 5.92 TB/s with 512 threads per row. Lines of 2-byte elements take 256 threads: the bf16 softmax rows (16 chunks each)
   // lose 3-4 % with 512, the bf16 [8192, 4096] rmsnorm rows run at 5.65 TB/s with 32 threads (16
   // chunks each) and 6.79 TB/s with 256 (2 each). Other widths: ~16 chunks per thread.
-  int target = V == 4 ? 8 : V == 8 ? (int)std::max<uint64_t>(1, (chunks + 255) / 256) : 16;
+  bool full_out = false;  // the line program stores a full-size output (a normalisation, softmax)
+  for (auto& op : R.outputs)
+    if (full(op.first)) full_out = true;
+  int target = V == 4 ? (full_out ? 2 : 8) : V == 8 ? (int)std::max<uint64_t>(1, (chunks + 255) / 256) : 16;
   if (const char* e = std::getenv("KURUMI_HIP_LINE_CHUNKS")) target = std::max(1, std::atoi(e));
   uint64_t t = 1;
   while (t < 1024 && t * (uint64_t)target < chunks) t *= 2;
