@@ -444,7 +444,10 @@ void Gen::plan_layout() {
   }
   if (flat) {
     TPL = 1;
-    WG = 256;
+    // one-wave groups for large streams (measured: SwiGLU gate 6.26-6.30 -> 6.47-6.50 TB/s, a
+    // 1 GiB copy 6.30 -> 6.42), 256 threads below 2M chunks (a 1M-chunk kernel ran 3 % slower)
+    WG = N / std::max(V, 1) >= ((uint64_t)1 << 21) ? 64 : 256;
+    if (const char* e = std::getenv("KURUMI_HIP_FLAT_WG")) WG = std::max(64, std::atoi(e) / 64 * 64);
     NC = 1;
     const char* fk = std::getenv("KURUMI_HIP_FLAT_CPT");
     FK = fk ? std::max(1, std::atoi(fk)) : 1;
