@@ -24,6 +24,7 @@
 #include <cstdint>
 #include <cstdlib>
 #include <stdexcept>
+#include <type_traits>
 
 #include "kernels.h"
 #include "numeric.h"
@@ -134,8 +135,6 @@ attn_mfma_k(AttnArgs a) {
   // raw buffer loads: rows past the sequence read as zero, no branches
   const uint32_t hb = (uint32_t)(S * D * 2);  // bytes per head
   const auto Q = rsrc(static_cast<const uint16_t*>(a.q) + base, hb);
-  const auto K = rsrc(static_cast<const uint16_t*>(a.k) + base, hb);
-  const auto V = rsrc(static_cast<const uint16_t*>(a.v) + base, hb);
 
   // Q fragments (B operand of S^T): lane holds query qw + 32u + qc, dims 16*s + 8*h .. +7
   u32x4 qf[QT][DS];
@@ -160,14 +159,18 @@ attn_mfma_k(AttnArgs a) {
   //      read touches do.
   auto kswz = [](int r) { return (r / W) % (16 / W); };
   auto vswz = [](int r) { return 4 * ((r / W) % (4 / W)); };
-  auto dma = [&](__amdgpu_buffer_rsrc_t src, int kb, KU_LDS unsigned char* dst, bool isv) {
+  // The block offset moves the descriptor's base (scalar work; the byte count shrinks with it, so
+  // blocks past the head still read zeros) and the per-lane offsets stay loop-invariant.
+  const uint16_t* kp = static_cast<const uint16_t*>(a.k) + base;
+  const uint16_t* vp = static_cast<const uint16_t*>(a.v) + base;
+  auto dma = [&](const uint16_t* src, int kb, KU_LDS unsigned char* dst, bool isv) {
     const uint32_t k0b = kb < nkb ? (uint32_t)kb * BK * RB : hb;
+    const auto R = rsrc(reinterpret_cast<const unsigned char*>(src) + k0b, hb - k0b);
 #pragma unroll
     for (int i = 0; i < NBLK; ++i) {
       const int blk = i * NW + wave, r = blk * (1024 / RB) + lane / CPR, pc = lane % CPR;
       const int cc = pc ^ (isv ? vswz(r) : kswz(r));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (KU_LDS void*)(dst + blk * 1024), 16,
-                                               (int)(k0b + r * RB + cc * 16), 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(R, (KU_LDS void*)(dst + blk * 1024), 16, r * RB + cc * 16, 0, 0, 0);
     }
   };
   auto kbuf = [&](int i) { return lds + i * TBYTES; };
@@ -205,17 +208,20 @@ attn_mfma_k(AttnArgs a) {
   const float c = a.scale * LOG2E;
   const bool live = qw < S;  // wave-uniform: waves past the sequence only help staging
 
-  dma(K, 0, kbuf(0), false);
-  dma(V, 0, vbuf(0), true);
-  dma(K, 1, kbuf(1), false);
+  dma(kp, 0, kbuf(0), false);
+  dma(vp, 0, vbuf(0), true);
+  dma(kp, 1, kbuf(1), false);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   // One block: softmax of sc (this block's S^T) and S^T of the next block into sn. The loop runs
   // two blocks per trip with the two score sets swapping roles, so no registers are copied.
-  auto block = [&](int kb, f32x16 (&sc)[QT][2], f32x16 (&sn)[QT][2]) __attribute__((always_inline)) {
+  // The parity of kb is a compile-time constant, so every LDS address is a loop-invariant
+  // per-lane value plus an immediate.
+  auto block = [&](int kb, f32x16 (&sc)[QT][2], f32x16 (&sn)[QT][2], auto par) __attribute__((always_inline)) {
+    constexpr int P = decltype(par)::value;
     // K of block kb+2 and V of block kb+1 into the buffers the previous block freed
-    dma(K, kb + 2, kbuf(kb & 1), false);
-    dma(V, kb + 1, vbuf((kb + 1) & 1), true);
+    dma(kp, kb + 2, kbuf(P), false);
+    dma(vp, kb + 1, vbuf(P ^ 1), true);
     const int64_t k0 = (int64_t)kb * BK;
     u32x4 pf[QT][4];
     if (live) {
@@ -257,7 +263,7 @@ attn_mfma_k(AttnArgs a) {
       // wave priority: the section that interleaves the next S^T MFMAs with this block's softmax
       // goes first when both waves of a SIMD are ready (measured 3 % faster than equal priority)
       __builtin_amdgcn_s_setprio(1);
-      s_mfma(kbuf((kb + 1) & 1), sn);
+      s_mfma(kbuf(P ^ 1), sn);
 #pragma unroll
       for (int u = 0; u < QT; ++u) {
         // the row sum adds the rounded probabilities (the ones the P.V product uses), two at a
@@ -281,7 +287,7 @@ attn_mfma_k(AttnArgs a) {
       // dims 4q..4q+3, and output lane i receives keys 0..3 of dim i. Two reads fetch exactly the
       // key groups the probability registers hold: 16s + 4h + 0..3 and 16s + 8 + 4h + 0..3.
       __builtin_amdgcn_s_setprio(0);
-      const KU_LDS unsigned char* LV = vbuf(kb & 1);
+      const KU_LDS unsigned char* LV = vbuf(P);
       const int g = lane >> 4, c16 = lane & 15;
 #pragma unroll
       for (int s = 0; s < 4; ++s)
@@ -307,8 +313,8 @@ attn_mfma_k(AttnArgs a) {
   f32x16 sa[QT][2], sb[QT][2];
   s_mfma(kbuf(0), sa);
   for (int kb = 0; kb < nkb; kb += 2) {
-    block(kb, sa, sb);
-    if (kb + 1 < nkb) block(kb + 1, sb, sa);
+    block(kb, sa, sb, std::integral_constant<int, 0>{});
+    if (kb + 1 < nkb) block(kb + 1, sb, sa, std::integral_constant<int, 1>{});
   }
 
 #pragma unroll
