@@ -4,10 +4,11 @@ The headline line (metric/value) is config 2 — row softmax over [8192, 32000] 
 primitives (reduce_max, sub, exp, sum, div) followed by argmax -> int32 — as HBM GB/s of the
 single fused kernel's algorithmic traffic. Every config runs as a device-resident plan
 (inputs uploaded once, threefry-seeded synthetic data generated on the device), W untimed
-launches, then K timed launches bracketed by stream synchronisation. Per-kernel durations
-come from hipEvents recorded on the plan's own stream. The other configs are reported under
-"configs" with their own roofline fractions; config "6" is the nn primitives around them
-(rope, the SwiGLU gate, rmsnorm, the int4 decode GEMV).
+launches, then K timed launches bracketed by hipEvents on the plan's own stream. The other
+configs are reported under "configs" with their own roofline fractions and CPU baselines;
+config "6" is the nn primitives around them (rope, the SwiGLU gate, rmsnorm, the int4
+QuantMatmul). The `make_*` functions build exactly the plans that are timed; the full-size GPU
+tests (tests/test_gpu_bench_configs.py) run those same plans and check their outputs.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,6] [--no-cpu]
 """
@@ -19,6 +20,7 @@ import os
 import sys
 import time
 from pathlib import Path
+from types import SimpleNamespace
 
 import numpy as np
 
@@ -51,53 +53,14 @@ def scaled_randn(std):
         [1] * len(s))), s))
 
 
-def time_plan(plan, steps: int, warmup: int, use_graph: bool = False):
-    """Warm up, then the timed region: `steps` back-to-back launches of the plan on its stream,
-    bracketed by hipEvents on that stream (ku_hip_plan_time) and by a host clock around the call,
-    which ends with the stream drained. Returns (wall ms per step, GPU ms of each plan step,
-    step labels): the GPU time per launch comes from the timed region's events; a following
-    run with events between the steps only splits it among the steps of a multi-kernel plan."""
-    for _ in range(warmup):
-        plan.launch(use_graph)
-    plan.sync()
-    t0 = time.perf_counter()
-    gpu_ms = plan.time(steps, use_graph)
-    wall_ms = (time.perf_counter() - t0) * 1e3 / steps
-    labels = plan.steps()
-    if len(labels) == 1:
-        return wall_ms, [gpu_ms], labels
-    shares = plan.time_steps(max(steps, 5))
-    tot = sum(shares)
-    per_step = [s / tot * gpu_ms for s in shares] if tot > 0 else shares
-    return wall_ms, per_step, labels
+def uniform_pm1(g, s, sd):
+    return g.rand_range(s, sd, -1.0, 1.0)
 
 
-def measured_traffic(kernel: str):
-    """HBM bytes per launch of a generated kernel, from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes (profiles/hbm_traffic.json, scaled by the copy-kernel calibration).
-    Keyed by the kernel's name, which hashes its source: a changed kernel reads as null."""
-    path = ROOT / "profiles" / "hbm_traffic.json"
-    if not path.exists():
-        return None
-    rec = json.loads(path.read_text()).get("kernels", {}).get(kernel)
-    return rec["traffic_bytes"] if rec else None
-
-
-def roofline_hbm(bytes_per_launch: float, kernel_ms: float, kernel: str | None = None):
-    gbs = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel) if kernel else None}
-
-
-def roofline_mfma(flops: float, kernel_ms: float, peak_tflops: float):
-    tf = flops / (kernel_ms * 1e-3) / 1e12
-    return {"bound": "mfma", "achieved": round(tf, 1), "peak": peak_tflops, "unit": "TFLOP/s",
-            "frac": round(tf / peak_tflops, 4), "traffic": None}
-
-
-# ---------------- config 2 (headline) ----------------
+# ---------------- the graphs and plans that are timed ----------------
 
 def softmax_graph(K, rows, cols, dt):
+    """cfg 2: softmax from primitives (reduce_max, sub, exp, sum, div), then argmax -> i32."""
     g = K.Graph()
     x = g.input([rows, cols], dt)
     m = g.reduce_max(x, 1)
@@ -108,85 +71,40 @@ def softmax_graph(K, rows, cols, dt):
     return g, x, y, a
 
 
-def bench_cfg2(hip, steps, warmup, dt_name="f32"):
+def cfg1_graph(K, n):
+    """cfg 1: sum over the last axis of relu(x*x + b) * 0.5."""
+    g = K.Graph()
+    x = g.input([n, n], K.DType.F32)
+    b = g.input([n], K.DType.F32)
+    h = g.mul(g.relu(g.add(g.mul(x, x), g.broadcast_to(b, [n, n]))), g.scalar(x, 0.5))
+    return g, x, b, g.sum(h, 1)
+
+
+def make_cfg1(hip, rep=0):
+    K = _ku()
+    n = 4096
+    g, x, b, y = cfg1_graph(K, n)
+    xt = device_values(hip, uniform_pm1, [n, n], 100 + rep, K.DType.F32)
+    bt = device_values(hip, uniform_pm1, [n], 200 + rep, K.DType.F32)
+    feeds = {x: xt, b: bt}
+    return SimpleNamespace(plan=hip.plan(g, [y], feeds), g=g, x=x, b=b, roots=[y], feeds=feeds,
+                           algo_bytes=4 * n * n + 4 * n + 4 * n)
+
+
+def make_cfg2(hip, dt_name="f32"):
     K = _ku()
     rows, cols = 8192, 32000
     dt = K.DType.F32 if dt_name == "f32" else K.DType.BF16
     xt = device_values(hip, scaled_randn(3.0), [rows, cols], 2024, dt)
     g, x, y, a = softmax_graph(K, rows, cols, dt)
-    plan = hip.plan(g, [y, a], {x: xt})
-    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    feeds = {x: xt}
     w = 4 if dt == K.DType.F32 else 2
-    algo_bytes = rows * cols * w * 2 + rows * 4  # read x, write y, write int32 argmax
-    kms = max(per_step)
-    k = per_step.index(kms)
-    return {
-        "workload": f"softmax+argmax [{rows},{cols}] {dt_name} (decomposed primitives)",
-        "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "dominant": labels[k],
-        "algo_bytes": algo_bytes, "value_gbs": algo_bytes / (wall_ms * 1e-3) / 1e9,
-        "roofline": roofline_hbm(algo_bytes, kms, labels[k]),
-        "_graph": (g, x, y, a, xt),
-    }
+    return SimpleNamespace(plan=hip.plan(g, [y, a], feeds), g=g, x=x, y=y, a=a, roots=[y, a], feeds=feeds,
+                           rows=rows, cols=cols, dt=dt,
+                           algo_bytes=rows * cols * w * 2 + rows * 4)  # read x, write y, write i32 argmax
 
 
-def cpu_baseline_cfg2(xt_full, rows_sample=256, cols=32000):
-    """The oracle (single-threaded C++ restatement of kurumi's interpreter) on a row sample."""
-    sys.path.insert(0, str(ROOT / "tests"))
-    import kutest
-    K = _ku()
-    x_all = xt_full.numpy()
-    xs = np.ascontiguousarray(x_all[:rows_sample])
-    g, x, y, a = softmax_graph(K, rows_sample, cols, K.DType.F32)
-    feeds = {x: K.Tensor.from_numpy(xs)}
-    kutest.interpret(g, [y, a], feeds)  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        kutest.interpret(g, [y, a], feeds)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > 8.0 or reps >= 20:
-            break
-    sec = el / reps
-    algo_bytes = rows_sample * cols * 8 + rows_sample * 4
-    return {"value": round(algo_bytes / sec / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{rows_sample} of 8192 rows x 32000 f32, decomposed softmax + argmax via the oracle "
-                      f"interpreter, {reps} reps, {sec * 1e3:.1f} ms/rep, host nproc={os.cpu_count()}"}
-
-
-# ---------------- other configs ----------------
-
-def bench_cfg1(hip, steps, warmup):
-    K = _ku()
-    n = 4096
-    plans = []
-    # rotate 5 input sets (5 x 64 MiB > 256 MiB MALL) so the kernel streams from HBM
-    for r in range(5):
-        g = K.Graph()
-        x = g.input([n, n], K.DType.F32)
-        b = g.input([n], K.DType.F32)
-        h = g.mul(g.relu(g.add(g.mul(x, x), g.broadcast_to(b, [n, n]))), g.scalar(x, 0.5))
-        y = g.sum(h, 1)
-        xt = device_values(hip, lambda gg, s, sd: gg.rand_range(s, sd, -1.0, 1.0), [n, n], 100 + r, K.DType.F32)
-        bt = device_values(hip, lambda gg, s, sd: gg.rand_range(s, sd, -1.0, 1.0), [n], 200 + r, K.DType.F32)
-        plans.append((hip.plan(g, [y], {x: xt, b: bt}), g))
-    for _ in range(warmup):
-        for p, _g in plans:
-            p.launch()
-    plans[0][0].sync()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        for p, _g in plans:
-            p.launch()
-    plans[0][0].sync()
-    wall_ms = (time.perf_counter() - t0) * 1e3 / (steps * len(plans))
-    algo_bytes = 4 * n * n + 4 * n + 4 * n
-    return {"workload": "sum_lastaxis(relu(x*x+b)*0.5) [4096,4096] f32, 5 rotating input sets",
-            "ms_per_step": wall_ms, "kernels": plans[0][0].steps(), "algo_bytes": algo_bytes,
-            "roofline": roofline_hbm(algo_bytes, wall_ms, plans[0][0].steps()[0])}
-
-
-def bench_gemm(hip, steps, warmup, batched=False):
-    K = _ku()
+def gemm_graph(K, batched):
     g = K.Graph()
     if batched:
         sa, sb, std = [8, 2048, 128], [8, 128, 2048], 1.0 / np.sqrt(128)
@@ -200,21 +118,21 @@ def bench_gemm(hip, steps, warmup, batched=False):
         b = g.input(sb, K.DType.BF16)
         c = g.matmul(a, b)
         flops = 2 * 4096 * 4096 * 11008
-    at = device_values(hip, scaled_randn(std), sa, 301, K.DType.BF16)
-    bt = device_values(hip, scaled_randn(std), sb, 302, K.DType.BF16)
-    plan = hip.plan(g, [c], {a: at, b: bt})
-    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
-    kms = next(t for t, l in zip(per_step, labels) if l.startswith("gemm"))
-    out = {"workload": ("batched [8,2048,128]@[8,128,2048]" if batched else "[4096,4096]@[4096,11008]") + " bf16",
-           "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "flops": flops,
-           "roofline": roofline_mfma(flops, kms, BF16_PEAK_TFLOPS)}
-    if batched:
-        byts = 2 * (8 * 2048 * 128 * 2) + 8 * 2048 * 2048 * 2
-        out["roofline_hbm"] = roofline_hbm(byts, kms)
-    return out
+    return g, a, b, c, sa, sb, std, flops
 
 
-def bench_attention(hip, steps, warmup):
+def make_gemm(hip, batched=False, rep=0):
+    K = _ku()
+    g, a, b, c, sa, sb, std, flops = gemm_graph(K, batched)
+    at = device_values(hip, scaled_randn(std), sa, 301 + 10 * rep, K.DType.BF16)
+    bt = device_values(hip, scaled_randn(std), sb, 302 + 10 * rep, K.DType.BF16)
+    feeds = {a: at, b: bt}
+    byts = 2 * (int(np.prod(sa)) + int(np.prod(sb))) + 2 * (int(np.prod(sa[:-1])) * sb[-1])
+    return SimpleNamespace(plan=hip.plan(g, [c], feeds), g=g, a=a, b=b, c=c, roots=[c], feeds=feeds,
+                           flops=flops, algo_bytes=byts)
+
+
+def make_attention(hip):
     K = _ku()
     B, H, S, D = 4, 32, 2048, 128
     g = K.Graph()
@@ -224,31 +142,151 @@ def bench_attention(hip, steps, warmup):
     o = g.sdpa(q, k, v, True)
     feeds = {n: device_values(hip, lambda gg, s, sd: gg.randn(s, sd), [B, H, S, D], 400 + i, K.DType.BF16)
              for i, n in enumerate([q, k, v])}
-    plan = hip.plan(g, [o], feeds)
-    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
-    flops = 4 * B * H * S * S * D // 2
-    return {"workload": "causal sdpa B4 H32 S2048 D128 bf16 (Op::Sdpa via g.sdpa)", "ms_per_step": wall_ms,
-            "kernels": labels, "kernel_ms": per_step, "flops": flops,
-            "roofline": roofline_mfma(flops, max(per_step), BF16_PEAK_TFLOPS)}
+    return SimpleNamespace(plan=hip.plan(g, [o], feeds), g=g, q=q, k=k, v=v, o=o, roots=[o], feeds=feeds,
+                           flops=4 * B * H * S * S * D // 2, algo_bytes=4 * B * H * S * D * 2)
 
 
-def bench_fp8(hip, steps, warmup):
+def fp8_graph(K, x_shape, w_f32: bytes, w_shape):
+    """cfg 5: a bf16 linear x @ W^T with an f32 weight constant, through the e4m3 pass (which
+    quantizes W per row from its stored f32 values and x per tensor in the graph)."""
+    g = K.Graph()
+    x = g.input(list(x_shape), K.DType.BF16)
+    w = g.constant_bytes(K.DType.F32, w_f32, list(w_shape))
+    y0 = g.dot_general(x, g.cast(w, K.DType.BF16), [1], [1])
+    return g, x, K.amp_fp8(g, y0)
+
+
+def make_fp8(hip):
     K = _ku()
     M, Kd, N = 2048, 4096, 11008
     wt = device_values(hip, scaled_randn(0.02), [N, Kd], 501, K.DType.F32)
-    g = K.Graph()
-    x = g.input([M, Kd], K.DType.BF16)
-    w = g.constant_bytes(K.DType.F32, wt.data, [N, Kd])
-    y0 = g.dot_general(x, g.cast(w, K.DType.BF16), [1], [1])
-    y = K.amp_fp8(g, y0)
+    g, x, y = fp8_graph(K, [M, Kd], wt.data, [N, Kd])
     xt = device_values(hip, lambda gg, s, sd: gg.randn(s, sd), [M, Kd], 502, K.DType.BF16)
-    plan = hip.plan(g, [y], {x: xt})
-    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
-    flops = 2 * M * N * Kd
-    gemm_ms = next(t for t, l in zip(per_step, labels) if l.startswith("gemm"))
+    feeds = {x: xt}
+    # Xq + Wq + sw + Y (bf16): the GEMM's algorithmic bytes
+    return SimpleNamespace(plan=hip.plan(g, [y], feeds), g=g, x=x, y=y, roots=[y], feeds=feeds, w=wt,
+                           M=M, K=Kd, N=N, flops=2 * M * N * Kd, algo_bytes=M * Kd + N * Kd + 4 * N + 2 * M * N)
+
+
+# ---------------- timing ----------------
+
+def time_plans(plans, steps: int, warmup: int, use_graph: bool = False):
+    """Warm up, then the timed region: `steps` rounds, each launching every plan once (rotating
+    independent input sets), bracketed by hipEvents on the plans' stream and by a host clock
+    around the call, which ends with the stream drained. Returns (wall ms per launch, GPU ms of
+    each step of a launch, step labels): the GPU time per launch comes from the timed region's
+    events; for a multi-kernel plan a following run with events between the steps splits it."""
+    K = _ku()
+    for _ in range(warmup):
+        for p in plans:
+            p.launch(use_graph)
+    plans[0].sync()
+    t0 = time.perf_counter()
+    gpu_ms = K.time_plans(plans, steps, use_graph) / len(plans)
+    wall_ms = (time.perf_counter() - t0) * 1e3 / (steps * len(plans))
+    labels = plans[0].steps()
+    if len(labels) == 1:
+        return wall_ms, [gpu_ms], labels
+    shares = plans[0].time_steps(max(steps, 5))
+    tot = sum(shares)
+    per_step = [s / tot * gpu_ms for s in shares] if tot > 0 else shares
+    return wall_ms, per_step, labels
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of a kernel, from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE
+    passes (profiles/hbm_traffic.json, scaled by the copy-kernel calibration). Keyed by the
+    kernel's plan label (generated kernels hash their source into it): a changed kernel reads
+    as null."""
+    path = ROOT / "profiles" / "hbm_traffic.json"
+    if not path.exists() or not kernel:
+        return None
+    rec = json.loads(path.read_text()).get("kernels", {}).get(kernel)
+    return rec["traffic_bytes"] if rec else None
+
+
+def roofline_hbm(bytes_per_launch: float, kernel_ms: float, kernel: str | None = None):
+    gbs = bytes_per_launch / (kernel_ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel)}
+
+
+def roofline_mfma(flops: float, kernel_ms: float, peak_tflops: float, kernel: str | None = None):
+    tf = flops / (kernel_ms * 1e-3) / 1e12
+    return {"bound": "mfma", "achieved": round(tf, 1), "peak": peak_tflops, "unit": "TFLOP/s",
+            "frac": round(tf / peak_tflops, 4), "traffic": measured_traffic(kernel)}
+
+
+def main_kernel(per_step, labels, prefix):
+    i = next(i for i, l in enumerate(labels) if l.startswith(prefix))
+    return per_step[i], labels[i]
+
+
+# ---------------- configs ----------------
+
+def bench_cfg2(hip, steps, warmup, dt_name="f32"):
+    c = make_cfg2(hip, dt_name)
+    wall_ms, per_step, labels = time_plans([c.plan], steps, warmup)
+    kms = max(per_step)
+    k = per_step.index(kms)
+    out = {
+        "workload": f"softmax+argmax [{c.rows},{c.cols}] {dt_name} (decomposed primitives)",
+        "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "dominant": labels[k],
+        "algo_bytes": c.algo_bytes, "value_gbs": c.algo_bytes / (wall_ms * 1e-3) / 1e9,
+        "roofline": roofline_hbm(c.algo_bytes, kms, labels[k]),
+    }
+    if dt_name == "f32":
+        # the same plan replayed as one hipGraph per launch (the ku_plan_run path)
+        gw, gper, _ = time_plans([c.plan], steps, warmup, use_graph=True)
+        out["graph_replay"] = {"ms_per_step": gw, "kernel_ms": gper[0],
+                               "gbs": c.algo_bytes / (gper[0] * 1e-3) / 1e9}
+        out["_cfg"] = c
+    return out
+
+
+def bench_cfg1(hip, steps, warmup):
+    # 5 rotating input sets (5 x 64 MiB > the 256 MiB last-level cache): the kernel streams from HBM
+    cs = [make_cfg1(hip, r) for r in range(5)]
+    wall_ms, per_step, labels = time_plans([c.plan for c in cs], steps, warmup)
+    return {"workload": "sum_lastaxis(relu(x*x+b)*0.5) [4096,4096] f32, 5 rotating input sets",
+            "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "algo_bytes": cs[0].algo_bytes,
+            "roofline": roofline_hbm(cs[0].algo_bytes, per_step[0], labels[0]), "_cfg": cs[0]}
+
+
+def bench_gemm(hip, steps, warmup, batched=False):
+    # the batched case (75 MB per set) rotates 4 input sets past the 256 MB last-level cache
+    cs = [make_gemm(hip, batched, r) for r in range(4 if batched else 1)]
+    wall_ms, per_step, labels = time_plans([c.plan for c in cs], steps, warmup)
+    kms, kl = main_kernel(per_step, labels, "gemm")
+    c = cs[0]
+    out = {"workload": ("batched [8,2048,128]@[8,128,2048]" if batched else "[4096,4096]@[4096,11008]") + " bf16"
+                       + (", 4 rotating input sets" if batched else ""),
+           "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "flops": c.flops,
+           "algo_bytes": c.algo_bytes, "roofline": roofline_mfma(c.flops, kms, BF16_PEAK_TFLOPS, kl), "_cfg": c}
+    if batched:
+        out["roofline_hbm"] = roofline_hbm(c.algo_bytes, kms, kl)
+    return out
+
+
+def bench_attention(hip, steps, warmup):
+    c = make_attention(hip)
+    wall_ms, per_step, labels = time_plans([c.plan], steps, warmup)
+    return {"workload": "causal sdpa B4 H32 S2048 D128 bf16 (Op::Sdpa via g.sdpa)", "ms_per_step": wall_ms,
+            "kernels": labels, "kernel_ms": per_step, "flops": c.flops,
+            "roofline": roofline_mfma(c.flops, max(per_step), BF16_PEAK_TFLOPS, labels[0]), "_cfg": c}
+
+
+def bench_fp8(hip, steps, warmup):
+    c = make_fp8(hip)
+    wall_ms, per_step, labels = time_plans([c.plan], steps, warmup)
+    gemm_ms, gl = main_kernel(per_step, labels, "gemm")
+    step_ms = sum(per_step)
     return {"workload": "e4m3 linear X[2048,4096] W[11008,4096]^T per-row/per-tensor scales, bf16 out",
-            "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "flops": flops,
-            "roofline": roofline_mfma(flops, gemm_ms, FP8_PEAK_TFLOPS)}
+            "ms_per_step": wall_ms, "kernels": labels, "kernel_ms": per_step, "flops": c.flops,
+            "roofline": roofline_mfma(c.flops, gemm_ms, FP8_PEAK_TFLOPS, gl),
+            "end_to_end": {"kernel_ms": step_ms, "tflops": round(c.flops / (step_ms * 1e-3) / 1e12, 1),
+                           "frac": round(c.flops / (step_ms * 1e-3) / 1e12 / FP8_PEAK_TFLOPS, 4)},
+            "_cfg": c}
 
 
 def bench_nn(hip, steps, warmup):
@@ -267,7 +305,7 @@ def bench_nn(hip, steps, warmup):
         feeds[x] = device_values(hip, scaled_randn(1.0), shp, 401 + r, K.DType.F32)
         roots.append(g.rope(x))
     plan = hip.plan(g, roots, feeds)
-    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    wall_ms, per_step, labels = time_plans([plan], steps, warmup)
     main = [i for i, l in enumerate(labels) if l.startswith("ku_ew_4x32x2048x128")]
     kms = sum(per_step[i] for i in main) / len(main)
     n = int(np.prod(shp))
@@ -287,7 +325,7 @@ def bench_nn(hip, steps, warmup):
                 feeds[t] = device_values(hip, scaled_randn(2.0), shape, 500 + 10 * r + i, K.DType.BF16)
             roots.append(build(g, ins))
         plan = hip.plan(g, roots, feeds)
-        wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+        wall_ms, per_step, labels = time_plans([plan], steps, warmup)
         kms = sum(per_step) / reps
         algo = bytes_per * int(np.prod(shape))
         out[name] = {"workload": ("silu(a) * b" if name == "nn_swiglu" else "rmsnorm(x, axis 1, 1e-6)") +
@@ -321,13 +359,13 @@ def bench_quant(hip, steps, warmup):
             roots.append(g.quant_matmul(x, qw, sc, None, 4, grp))
         xt = device_values(hip, scaled_randn(1.0), [m, k], 601, K.DType.BF16)
         plan = hip.plan(g, roots, {x: xt})
-        wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+        wall_ms, per_step, labels = time_plans([plan], steps, warmup)
         kms = sum(per_step) / layers
         algo = n * k // 2 + n * (k // grp) * 2 + m * k * 2 + m * n * 2  # packed weight, scales, act, out
         out[key] = {"workload": f"int4 (sym, group {grp}) {what} [{m},{k}] x [{n},{k}]^T bf16, "
                                f"{layers} layers' weights per plan", "ms_per_step": wall_ms / layers,
                     "kernels": labels[:1], "kernel_ms": per_step[:1], "algo_bytes": algo,
-                    "roofline": roofline_hbm(algo, kms)}
+                    "roofline": roofline_hbm(algo, kms, labels[0])}
     return out
 
 
@@ -340,9 +378,106 @@ def bench_copy(hip, steps, warmup):
     y = g.neg(g.neg(x))
     xt = device_values(hip, lambda gg, s, sd: gg.rand_uniform(s, sd), [n // 4096, 4096], 7, K.DType.F32)
     plan = hip.plan(g, [y], {x: xt})
-    wall_ms, per_step, labels = time_plan(plan, steps, warmup)
+    wall_ms, per_step, labels = time_plans([plan], steps, warmup)
     return {"workload": "copy 1 GiB f32 (y = -(-x))", "kernels": labels, "kernel_ms": per_step,
-            "algo_bytes": 2 * 4 * n, "roofline": roofline_hbm(2 * 4 * n, max(per_step))}
+            "algo_bytes": 2 * 4 * n, "roofline": roofline_hbm(2 * 4 * n, max(per_step), labels[0])}
+
+
+# ---------------- CPU baselines (the oracle: single-threaded C++ restatement of kurumi's CPU paths) ----------------
+
+def _oracle():
+    sys.path.insert(0, str(ROOT / "tests"))
+    import kutest
+
+    return kutest
+
+
+def _time_cpu(fn, budget_s, max_reps=20):
+    fn()  # warm-up
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= max_reps:
+            return el / reps, reps
+
+
+def _cpu_line(value, unit, sample, reps, sec):
+    return {"value": value, "unit": unit, "cores": 1, "kind": "port",
+            "sample": f"{sample}; {reps} reps, {sec * 1e3:.1f} ms/rep; host nproc={os.cpu_count()}"}
+
+
+def cpu_baseline_cfg2(xt_full, rows_sample=256, cols=32000):
+    """The oracle interpreter on a row sample of the same logits (rows are independent)."""
+    kt, K = _oracle(), _ku()
+    xs = np.ascontiguousarray(xt_full.numpy()[:rows_sample])
+    g, x, y, a = softmax_graph(K, rows_sample, cols, K.DType.F32)
+    feeds = {x: K.Tensor.from_numpy(xs)}
+    sec, reps = _time_cpu(lambda: kt.interpret(g, [y, a], feeds), 8.0)
+    algo_bytes = rows_sample * cols * 8 + rows_sample * 4
+    return _cpu_line(round(algo_bytes / sec / 1e9, 4), "GB/s",
+                     f"{rows_sample} of 8192 rows x 32000 f32, decomposed softmax + argmax via the oracle "
+                     f"interpreter", reps, sec)
+
+
+def cpu_baseline_cfg1(c):
+    """The view-fused CPU path (restated realize::force) on the full cfg 1 input."""
+    kt = _oracle()
+    sec, reps = _time_cpu(lambda: kt.realize(c.g, c.roots[0], c.feeds), 4.0)
+    return _cpu_line(round(c.algo_bytes / sec / 1e9, 4), "GB/s",
+                     "full [4096,4096] f32 through the view-fused realize path", reps, sec)
+
+
+def cpu_baseline_gemm(c, batched):
+    """The oracle interpreter's contraction on a stated sub-shape (f32 accumulate, bf16 out),
+    reported as GFLOP/s of that sub-shape (the work is linear in the rows)."""
+    kt, K = _oracle(), _ku()
+    g = K.Graph()
+    if batched:
+        sa, sb = [1, 256, 128], [1, 128, 2048]
+        a, b = g.input(sa, K.DType.BF16), g.input(sb, K.DType.BF16)
+        y = g.dot_general(a, b, [2], [1], [0], [0])
+        src_a = c.feeds[c.a].numpy()[:1, :256]
+        src_b = c.feeds[c.b].numpy()[:1]
+    else:
+        sa, sb = [8, 4096], [4096, 11008]
+        a, b = g.input(sa, K.DType.BF16), g.input(sb, K.DType.BF16)
+        y = g.matmul(a, b)
+        src_a = c.feeds[c.a].numpy()[:8]
+        src_b = c.feeds[c.b].numpy()
+    feeds = {a: K.Tensor(K.DType.BF16, sa, np.ascontiguousarray(src_a).tobytes()),
+             b: K.Tensor(K.DType.BF16, sb, np.ascontiguousarray(src_b).tobytes())}
+    sec, reps = _time_cpu(lambda: kt.interpret(g, [y], feeds), 4.0, 5)
+    flops = 2 * int(np.prod(sa)) * sb[-1]
+    return _cpu_line(round(flops / sec / 1e9, 4), "GFLOP/s",
+                     f"{sa}@{sb} bf16 (sub-shape of the config) via the oracle interpreter", reps, sec)
+
+
+def cpu_baseline_attention(c):
+    """The oracle's sdpa on one of the 128 (batch, head) slices, causal."""
+    kt, K = _oracle(), _ku()
+    S, D = 2048, 128
+    g = K.Graph()
+    q, k, v = (g.input([1, 1, S, D], K.DType.BF16) for _ in range(3))
+    o = g.sdpa_fused(q, k, v, True)
+    feeds = {n: K.Tensor(K.DType.BF16, [1, 1, S, D], np.ascontiguousarray(c.feeds[src].numpy()[:1, :1]).tobytes())
+             for n, src in ((q, c.q), (k, c.k), (v, c.v))}
+    sec, reps = _time_cpu(lambda: kt.interpret(g, [o], feeds), 4.0, 3)
+    flops = 4 * S * S * D // 2
+    return _cpu_line(round(flops / sec / 1e9, 4), "GFLOP/s",
+                     "one (batch, head) slice [1,1,2048,128] bf16 causal via the oracle interpreter", reps, sec)
+
+
+def cpu_baseline_fp8(c, rows=8):
+    """The oracle interpreter on the e4m3 graph with `rows` activation rows."""
+    kt, K = _oracle(), _ku()
+    g, x, y = fp8_graph(K, [rows, c.K], c.w.data, [c.N, c.K])
+    feeds = {x: K.Tensor(K.DType.BF16, [rows, c.K], np.ascontiguousarray(c.feeds[c.x].numpy()[:rows]).tobytes())}
+    sec, reps = _time_cpu(lambda: kt.interpret(g, [y], feeds), 4.0, 5)
+    flops = 2 * rows * c.N * c.K
+    return _cpu_line(round(flops / sec / 1e9, 4), "GFLOP/s",
+                     f"[{rows},{c.K}] x [{c.N},{c.K}]^T e4m3 linear (sub-shape) via the oracle interpreter", reps, sec)
 
 
 def main() -> int:
@@ -364,21 +499,19 @@ def main() -> int:
     hip = K.HipBackend()
     cfgs = {c.strip() for c in args.configs.split(",") if c.strip()}
     head = bench_cfg2(hip, args.steps, args.warmup, "f32")
-    g, x, y, a, xt = head.pop("_graph")
+    hc = head.pop("_cfg")
     extra = {}
     if "2" in cfgs:
-        b16 = bench_cfg2(hip, args.steps, args.warmup, "bf16")
-        b16.pop("_graph")
-        extra["cfg2_bf16"] = b16
+        extra["cfg2_bf16"] = bench_cfg2(hip, args.steps, args.warmup, "bf16")
     if "1" in cfgs:
         extra["cfg1"] = bench_cfg1(hip, args.steps, args.warmup)
     if "3" in cfgs:
-        extra["cfg3"] = bench_gemm(hip, max(3, args.steps // 4), 1)
+        extra["cfg3"] = bench_gemm(hip, args.steps, args.warmup)
         extra["cfg3b"] = bench_gemm(hip, args.steps, args.warmup, batched=True)
     if "4" in cfgs:
-        extra["cfg4"] = bench_attention(hip, max(3, args.steps // 4), 1)
+        extra["cfg4"] = bench_attention(hip, args.steps, args.warmup)
     if "5" in cfgs:
-        extra["cfg5"] = bench_fp8(hip, max(3, args.steps // 4), 1)
+        extra["cfg5"] = bench_fp8(hip, args.steps, args.warmup)
     if "6" in cfgs:
         extra.update(bench_nn(hip, args.steps, args.warmup))
         extra.update(bench_quant(hip, args.steps, args.warmup))
@@ -387,14 +520,24 @@ def main() -> int:
     # the same step through the host boundary (ku_eval_many with host feeds -> host results):
     # PCIe-inclusive rate, reported beside the device-resident value (last: the GPU idles while
     # the host copies, which would cool the clocks for the device-resident configs)
-    hip.eval_many_with(g, [y, a], {x: xt})
+    xt = hc.feeds[hc.x]
+    hip.eval_many_with(hc.g, hc.roots, {hc.x: xt})
     t0 = time.perf_counter()
     for _ in range(2):
-        hip.eval_many_with(g, [y, a], {x: xt})
+        hip.eval_many_with(hc.g, hc.roots, {hc.x: xt})
     host_ms = (time.perf_counter() - t0) * 1e3 / 2
     extra["cfg2_host_io"] = {"workload": "cfg 2 f32 via ku_eval_many (host feeds in, host tensors out)",
                              "ms_per_step": host_ms, "gbs": head["algo_bytes"] / (host_ms * 1e-3) / 1e9}
-    cpu = None if args.no_cpu else cpu_baseline_cfg2(xt)
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_cfg2(xt)
+        for key, fn in (("cfg1", lambda c: cpu_baseline_cfg1(c)), ("cfg3", lambda c: cpu_baseline_gemm(c, False)),
+                        ("cfg3b", lambda c: cpu_baseline_gemm(c, True)), ("cfg4", cpu_baseline_attention),
+                        ("cfg5", cpu_baseline_fp8)):
+            if key in extra:
+                extra[key]["cpu_baseline"] = fn(extra[key]["_cfg"])
+    for v in extra.values():
+        v.pop("_cfg", None)
     line = {
         "metric": "fused softmax+argmax HBM GB/s (cfg 2, f32 [8192,32000]); GEMM/attn TFLOP/s under configs",
         "value": round(head["value_gbs"], 1),
@@ -415,6 +558,7 @@ def main() -> int:
         "configs": {k: {kk: (round(vv, 4) if isinstance(vv, float) else vv) for kk, vv in v.items()}
                     for k, v in extra.items()},
     }
+    line["configs"]["cfg2_graph_replay"] = head["graph_replay"]
     print(json.dumps(line))
     return 0
 

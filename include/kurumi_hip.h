@@ -170,8 +170,8 @@ size_t ku_graph_serialize_multi(const KuGraph *g, size_t n_entries, const char *
                                 const KuNode *in_nodes, const uint8_t *in_roles, const char *const *in_names,
                                 uint8_t *out, size_t cap);
 /* NULL (see ku_last_error) on a malformed or entry-less blob; every node is replayed through
- * the checked builders. Ops outside this IR (QuantMatmul, linalg, complex, gather/scatter,
- * argsort) are rejected with their name. */
+ * the checked builders. Ops outside this IR (linalg, complex, gather/scatter, argsort) are
+ * rejected with their name; QuantMatmul (tag 40) decodes like any other op. */
 KuRunnable *ku_graph_deserialize(const uint8_t *bytes, size_t len);
 KuGraph *ku_runnable_take_graph(KuRunnable *h);
 size_t ku_runnable_output_count(const KuRunnable *h);
@@ -190,8 +190,11 @@ uint32_t ku_runnable_entry_input_role(const KuRunnable *h, size_t i, size_t j);
 size_t ku_runnable_entry_input_name(const KuRunnable *h, size_t i, size_t j, uint8_t *out, size_t cap);
 void ku_runnable_free(KuRunnable *h);
 
-/* plan-replay: kurumi.h:456-458. Here the plan is a device plan on the process's default
- * KU_HIP backend (device 0), replayed as one hipGraph launch per run. */
+/* plan-replay: kurumi.h:456-458. Here the plan is a device plan, replayed as one hipGraph
+ * launch per run. ku_plan_compile has no backend argument, so its plans live on a
+ * process-default KU_HIP backend (device 0) that is created on first use and never destroyed
+ * (its device memory is returned when the process ends). ku_plan_run requires the graph the
+ * plan was compiled on, or one with the same content. */
 KuPlan *ku_plan_compile(const KuGraph *g, KuNode node);
 KuTensor *ku_plan_run(const KuPlan *p, const KuGraph *g, const KuFeeds *feeds);
 void ku_plan_free(KuPlan *p);
@@ -225,6 +228,10 @@ KuNode ku_sdpa_fused(KuGraph *g, KuNode q, KuNode k, KuNode v, uint32_t causal);
  * next to kurumi.h:395 ku_amp, which is f16-only). Returns the new root or KU_ERR. */
 KuNode ku_amp_fp8(KuGraph *g, KuNode root);
 
+/* ku_plan_compile on a caller's backend, sharing its plan and constant caches; run and free
+ * with ku_plan_run / ku_plan_free. */
+KuPlan *ku_hip_plan_compile_on(const KuBackend *b, const KuGraph *g, KuNode node);
+
 /* Device-resident plan: compile `roots`, upload `feeds` once, then launch repeatedly with
  * inputs and outputs staying in HBM. The graph must outlive the plan. */
 KuHipPlan *ku_hip_plan_new(KuGraph *g, const KuNode *roots, size_t n, const KuBackend *backend,
@@ -240,6 +247,9 @@ size_t ku_hip_plan_step_label(const KuHipPlan *p, size_t i, char *out, size_t ca
 int32_t ku_hip_plan_time_steps(KuHipPlan *p, int32_t iters, double *out_ms, size_t cap);
 /* Average GPU milliseconds of a whole plan launch over `iters` runs. */
 double ku_hip_plan_time(KuHipPlan *p, int32_t iters, uint32_t use_graph);
+/* Average GPU milliseconds of one round that launches each of `n` plans (one backend) once,
+ * in order, over `iters` rounds: rotating independent input sets through the same kernels. */
+double ku_hip_plans_time(KuHipPlan *const *plans, size_t n, int32_t iters, uint32_t use_graph);
 void ku_hip_plan_free(KuHipPlan *p);
 
 /* Generated HIP source of every fused region kernel for `roots`, concatenated and
@@ -247,8 +257,10 @@ void ku_hip_plan_free(KuHipPlan *p);
  * compile != 0). Returns the byte length; copies at most cap bytes into out. */
 size_t ku_hip_codegen(KuGraph *g, const KuNode *roots, size_t n, uint32_t compile, uint8_t *out, size_t cap);
 
-/* Dispatch counters of a backend: launches per kind (fused, gemm, attention, upload,
- * download) into out[0..5]; returns the number of evals. */
+/* Counters of a backend into out[0..cap): launches per kind (fused, gemm, attention, upload,
+ * download), then plans built, constants uploaded and constants cached (plans and constants
+ * are cached by graph content, so an equal graph rebuilt per call adds to neither); returns
+ * the number of evals. */
 uint64_t ku_hip_profile(const KuBackend *b, uint64_t *out_launches, size_t cap);
 
 #ifdef __cplusplus

@@ -15,7 +15,7 @@ from typing import Iterable, Sequence
 
 import numpy as np
 
-__all__ = ["DType", "Graph", "HipBackend", "Tensor", "KuError", "lib", "amp_fp8", "KU_ERR"]
+__all__ = ["DType", "Graph", "HipBackend", "Plan", "Tensor", "KuError", "lib", "amp_fp8", "KU_ERR"]
 
 _PKG = Path(__file__).resolve().parent
 _LIB_PATH = _PKG / "libkurumi_hip.so"
@@ -122,6 +122,7 @@ def _declare(L: C.CDLL) -> None:
         "ku_plan_compile": ([P, u32], P),
         "ku_plan_run": ([P, P, P], P),
         "ku_plan_free": ([P], None),
+        "ku_hip_plan_compile_on": ([P, P, u32], P),
         "ku_feeds_new": ([], P),
         "ku_feeds_free": ([P], None),
         "ku_feeds_set": ([P, u32, P], None),
@@ -145,6 +146,7 @@ def _declare(L: C.CDLL) -> None:
         "ku_hip_plan_time_steps": ([P, C.c_int32, C.POINTER(C.c_double), sz], C.c_int32),
         "ku_hip_plan_time": ([P, C.c_int32, u32], C.c_double),
         "ku_hip_plan_free": ([P], None),
+        "ku_hip_plans_time": ([C.POINTER(P), sz, C.c_int32, u32], C.c_double),
         "ku_hip_codegen": ([P, C.POINTER(C.c_uint32), sz, u32, C.c_char_p, sz], sz),
         "ku_hip_profile": ([P, C.POINTER(C.c_uint64), sz], C.c_uint64),
         "ku_quant_matmul": ([P, u32, u32, u32, u32, C.c_uint8, sz], u32),
@@ -622,6 +624,15 @@ class HipPlan:
         if not self.h:
             raise KuError(f"ku_hip_plan_new: {last_error()}")
 
+    def feed(self, node: int, t: Tensor) -> None:
+        """Upload a new value for one Input (same shape and dtype) into the plan's buffer."""
+        th = t._handle()
+        try:
+            if lib().ku_hip_plan_feed(self.h, int(node), th) != 0:
+                raise KuError(f"ku_hip_plan_feed: {last_error()}")
+        finally:
+            lib().ku_tensor_free(th)
+
     def launch(self, use_graph: bool = False) -> None:
         if lib().ku_hip_plan_launch(self.h, int(use_graph)) != 0:
             raise KuError(f"ku_hip_plan_launch: {last_error()}")
@@ -662,6 +673,15 @@ class HipPlan:
         if getattr(self, "h", None) and _lib is not None:
             _lib.ku_hip_plan_free(self.h)
             self.h = None
+
+
+def time_plans(plans: Sequence[HipPlan], iters: int, use_graph: bool = False) -> float:
+    """Average GPU ms of one round launching every plan once (ku_hip_plans_time)."""
+    arr = (C.c_void_p * len(plans))(*[p.h for p in plans])
+    ms = lib().ku_hip_plans_time(arr, len(plans), iters, int(use_graph))
+    if ms < 0:
+        raise KuError(f"ku_hip_plans_time: {last_error()}")
+    return ms
 
 
 class HipBackend:
@@ -705,7 +725,39 @@ class HipBackend:
     def plan(self, g: Graph, roots: Sequence[int], feeds: dict[int, Tensor]) -> HipPlan:
         return HipPlan(self, g, roots, feeds)
 
+    def compile(self, g: Graph, node: int) -> "Plan":
+        """kurumi.h:456 ku_plan_compile on this backend (ku_hip_plan_compile_on)."""
+        return Plan(g, node, self)
+
     def profile(self) -> dict:
-        arr = (C.c_uint64 * 5)()
-        evals = lib().ku_hip_profile(self.h, arr, 5)
-        return {"evals": evals, **dict(zip(["fused", "gemm", "attention", "upload", "download"], list(arr)))}
+        keys = ["fused", "gemm", "attention", "upload", "download", "plans_built", "const_uploads", "const_entries"]
+        arr = (C.c_uint64 * len(keys))()
+        evals = lib().ku_hip_profile(self.h, arr, len(keys))
+        return {"evals": evals, **dict(zip(keys, list(arr)))}
+
+
+class Plan:
+    """Compile once, run per feeds (kurumi_core/src/realize/plan.rs:13-58; C ABI kurumi.h:455-458).
+    Here a device plan replayed as one hipGraph launch per run. Without a backend it lives on the
+    process-default KU_HIP backend (``ku_plan_compile``)."""
+
+    def __init__(self, g: Graph, node: int, backend: "HipBackend | None" = None):
+        self._b = backend
+        if backend is None:
+            self.h = lib().ku_plan_compile(g.h, node)
+        else:
+            self.h = lib().ku_hip_plan_compile_on(backend.h, g.h, node)
+        if not self.h:
+            raise KuError(f"ku_plan_compile: {last_error()}")
+
+    def run(self, g: Graph, feeds: dict[int, Tensor]) -> Tensor:
+        f = Feeds(feeds)
+        h = lib().ku_plan_run(self.h, g.h, f.h)
+        if not h:
+            raise KuError(f"ku_plan_run: {last_error()}")
+        return Tensor._from_handle(h)
+
+    def __del__(self):
+        if getattr(self, "h", None) and _lib is not None:
+            _lib.ku_plan_free(self.h)
+            self.h = None

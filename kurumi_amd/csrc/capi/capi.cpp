@@ -21,7 +21,12 @@ using ku::NodeId;
 using ku::Shape;
 
 struct KuBackend { std::unique_ptr<ku::hipbk::HipBackend> b; };
-struct KuPlan { std::shared_ptr<ku::hipbk::Plan> p; std::vector<NodeId> inputs; };
+struct KuPlan {
+  std::shared_ptr<ku::hipbk::Plan> p;
+  uint64_t gid;              // the graph it was compiled on
+  ku::hipbk::Hash128 fp;     // and that graph's content, for a run on an equal graph
+  NodeId node;
+};
 struct KuHipPlan { std::unique_ptr<ku::hipbk::Plan> p; ku::hipbk::HipBackend* b; };
 
 namespace {
@@ -58,13 +63,30 @@ ku::DType to_dt(uint32_t d) {
   return static_cast<ku::DType>(d);
 }
 
-// process-default HIP backend for ku_plan_* (whose reference signature has no backend)
+// Process-default HIP backend (device 0) for ku_plan_compile, whose reference signature has no
+// backend. Created on first use and deliberately never destroyed: static destructors run after
+// the HIP runtime may have begun tearing down, and plans still held by the caller point into
+// it. The driver returns its device memory when the process ends.
 std::mutex g_default_mu;
-std::unique_ptr<ku::hipbk::HipBackend> g_default;
+ku::hipbk::HipBackend* g_default = nullptr;
 ku::hipbk::HipBackend* default_backend() {
   std::lock_guard<std::mutex> lk(g_default_mu);
-  if (!g_default) g_default = std::make_unique<ku::hipbk::HipBackend>(0);
-  return g_default.get();
+  if (!g_default) g_default = new ku::hipbk::HipBackend(0);
+  return g_default;
+}
+
+KuPlan* compile_plan(ku::hipbk::HipBackend* b, const ku::Graph& g, KuNode node) {
+  auto* p = new KuPlan();
+  try {
+    p->p = b->plan_for(g, {node});
+    p->gid = g.id();
+    p->fp = ku::hipbk::graph_fingerprint(g, {node});
+    p->node = node;
+  } catch (...) {
+    delete p;
+    throw;
+  }
+  return p;
 }
 
 }  // namespace
@@ -225,6 +247,7 @@ KuNode ku_flip(KuGraph* g, KuNode x, const size_t* axes, size_t n) {
 }
 KuNode ku_slice(KuGraph* g, KuNode x, const size_t* ranges, size_t rank) {
   return build(g, "ku_slice", [&](ku::Graph& gr) {
+    if (!ranges && rank) throw ku::Error("ku_slice: null ranges");
     std::vector<ku::SliceRange> r;
     for (size_t i = 0; i < rank; ++i) r.push_back({ranges[2 * i], ranges[2 * i + 1], 1});
     return gr.slice(x, r);
@@ -232,6 +255,7 @@ KuNode ku_slice(KuGraph* g, KuNode x, const size_t* ranges, size_t rank) {
 }
 KuNode ku_slice_step(KuGraph* g, KuNode x, const size_t* ranges, size_t rank) {
   return build(g, "ku_slice_step", [&](ku::Graph& gr) {
+    if (!ranges && rank) throw ku::Error("ku_slice_step: null ranges");
     std::vector<ku::SliceRange> r;
     for (size_t i = 0; i < rank; ++i) r.push_back({ranges[3 * i], ranges[3 * i + 1], ranges[3 * i + 2]});
     return gr.slice(x, r);
@@ -239,6 +263,7 @@ KuNode ku_slice_step(KuGraph* g, KuNode x, const size_t* ranges, size_t rank) {
 }
 KuNode ku_pad(KuGraph* g, KuNode x, const size_t* pads, size_t rank) {
   return build(g, "ku_pad", [&](ku::Graph& gr) {
+    if (!pads && rank) throw ku::Error("ku_pad: null pads");
     std::vector<ku::PadRange> p;
     for (size_t i = 0; i < rank; ++i) p.push_back({pads[2 * i], pads[2 * i + 1]});
     return gr.pad(x, p);
@@ -389,12 +414,14 @@ KuPlan* ku_plan_compile(const KuGraph* g, KuNode node) {
     set_err("ku_plan_compile: null graph handle");
     return nullptr;
   }
-  return guard<KuPlan*>(nullptr, [&] {
-    auto* b = default_backend();
-    auto* p = new KuPlan();
-    p->p = std::shared_ptr<ku::hipbk::Plan>(b->new_plan(g->g, {node}).release());
-    return p;
-  });
+  return guard<KuPlan*>(nullptr, [&] { return compile_plan(default_backend(), g->g, node); });
+}
+KuPlan* ku_hip_plan_compile_on(const KuBackend* b, const KuGraph* g, KuNode node) {
+  if (!b || !g) {
+    set_err("ku_hip_plan_compile_on: null backend/graph handle");
+    return nullptr;
+  }
+  return guard<KuPlan*>(nullptr, [&] { return compile_plan(b->b.get(), g->g, node); });
 }
 KuTensor* ku_plan_run(const KuPlan* p, const KuGraph* g, const KuFeeds* feeds) {
   if (!p || !g || !feeds) {
@@ -402,6 +429,10 @@ KuTensor* ku_plan_run(const KuPlan* p, const KuGraph* g, const KuFeeds* feeds) {
     return nullptr;
   }
   return guard<KuTensor*>(nullptr, [&] {
+    // realize/plan.rs:45: `g` must be the graph the plan was compiled on (or an equal one)
+    if (g->g.id() != p->gid &&
+        (p->node >= g->g.size() || ku::hipbk::graph_fingerprint(g->g, {p->node}) != p->fp))
+      throw ku::Error("ku_plan_run: the plan was compiled on a different graph");
     ku::hipbk::feed_plan(*p->p, feeds->f);
     p->p->launch(true);
     return new KuTensor{p->p->download(0)};
@@ -420,6 +451,7 @@ void ku_feeds_set(KuFeeds* f, KuNode node, const KuTensor* t) {
 
 KuTensor* ku_tensor_f32(const float* data, size_t len, const size_t* shape, size_t rank) {
   return guard<KuTensor*>(nullptr, [&] {
+    if (!data && len) throw ku::Error("ku_tensor_f32: null data");  // capi/tensor.rs:57-60
     Shape s = mk_shape(shape, rank);
     if (ku::numel(s) != len) throw ku::Error("ku_tensor_f32: len does not match shape");
     auto* t = new KuTensor();
@@ -432,6 +464,7 @@ KuTensor* ku_tensor_f32(const float* data, size_t len, const size_t* shape, size
 }
 KuTensor* ku_tensor_new(uint32_t dtype, const uint8_t* data, size_t nbytes, const size_t* shape, size_t rank) {
   return guard<KuTensor*>(nullptr, [&] {
+    if (!data && nbytes) throw ku::Error("ku_tensor_new: null data");
     ku::DType dt = to_dt(dtype);
     Shape s = mk_shape(shape, rank);
     if (ku::numel(s) * ku::dt_width(dt) != nbytes) throw ku::Error("ku_tensor_new: nbytes does not match shape");
@@ -554,6 +587,34 @@ double ku_hip_plan_time(KuHipPlan* p, int32_t iters, uint32_t use_graph) {
     return static_cast<double>(ms) / std::max(iters, 1);
   });
 }
+double ku_hip_plans_time(KuHipPlan* const* plans, size_t n, int32_t iters, uint32_t use_graph) {
+  if (!plans || !n) {
+    set_err("ku_hip_plans_time: no plans");
+    return -1.0;
+  }
+  for (size_t i = 0; i < n; ++i)
+    if (!plans[i] || plans[i]->b != plans[0]->b) {
+      set_err("ku_hip_plans_time: null plan, or plans on different backends");
+      return -1.0;
+    }
+  return guard<double>(-1.0, [&] {
+    auto& ctx = plans[0]->b->ctx();
+    ctx.make_current();
+    hipEvent_t e0, e1;
+    KU_HIP(hipEventCreate(&e0));
+    KU_HIP(hipEventCreate(&e1));
+    KU_HIP(hipEventRecord(e0, ctx.stream()));
+    for (int i = 0; i < iters; ++i)
+      for (size_t j = 0; j < n; ++j) plans[j]->p->launch(use_graph != 0);
+    KU_HIP(hipEventRecord(e1, ctx.stream()));
+    KU_HIP(hipEventSynchronize(e1));
+    float ms = 0.f;
+    KU_HIP(hipEventElapsedTime(&ms, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    return static_cast<double>(ms) / std::max(iters, 1);
+  });
+}
 void ku_hip_plan_free(KuHipPlan* p) { delete p; }
 
 size_t ku_hip_codegen(KuGraph* g, const KuNode* roots, size_t n, uint32_t compile, uint8_t* out, size_t cap) {
@@ -578,7 +639,9 @@ size_t ku_hip_codegen(KuGraph* g, const KuNode* roots, size_t n, uint32_t compil
 uint64_t ku_hip_profile(const KuBackend* b, uint64_t* out, size_t cap) {
   if (!b) return 0;
   auto& pr = b->b->ctx().profile();
-  for (size_t i = 0; i < cap && i < (size_t)ku::hipbk::Kind::NumKinds; ++i) out[i] = pr.launches[i];
+  const size_t nk = (size_t)ku::hipbk::Kind::NumKinds;
+  uint64_t extra[3] = {b->b->plans_built(), b->b->consts().uploads(), b->b->consts().entries()};
+  for (size_t i = 0; out && i < cap && i < nk + 3; ++i) out[i] = i < nk ? pr.launches[i] : extra[i - nk];
   return pr.evals;
 }
 

@@ -7,6 +7,7 @@
 #include <memory>
 
 #include "../ir/tensor.h"
+#include "fingerprint.h"
 #include "plan.h"
 #include "runtime.h"
 
@@ -19,8 +20,11 @@ class HipBackend : public ku::Backend {
   const char* name() const override { return "hip"; }
   std::vector<Tensor> eval_many(const Graph& g, const std::vector<NodeId>& ids, const Feeds& feeds) override;
 
-  // A device plan for `roots` (cached per graph id + roots + graph size).
+  // A device plan for `roots`, cached by (graph id, graph size, roots) and, on a miss there,
+  // by the content fingerprint of the reachable subgraph, so an identical graph rebuilt per
+  // call (the KGPH v2 seam) reuses the plan and its uploaded constants.
   std::shared_ptr<Plan> plan_for(const Graph& g, const std::vector<NodeId>& roots);
+  size_t plans_built() const { return plans_built_; }
   std::unique_ptr<Plan> new_plan(const Graph& g, const std::vector<NodeId>& roots);
   Context& ctx() { return *ctx_; }
   ConstCache& consts() { return *consts_; }
@@ -32,9 +36,11 @@ class HipBackend : public ku::Backend {
     uint64_t gid;
     size_t gsize;
     std::vector<NodeId> roots;
+    Hash128 fp;
     std::shared_ptr<Plan> plan;
   };
   std::list<Entry> plans_;  // most recent first
+  size_t plans_built_ = 0;
 };
 
 void feed_plan(Plan& p, const Feeds& feeds);

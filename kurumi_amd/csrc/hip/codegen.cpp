@@ -427,8 +427,13 @@ void Gen::plan_layout() {
   bool contiguous_axis = flat || inner == 1;
   for (auto& l : R.leaves)
     if (l.view.strides[vecaxis] != 0) minw = std::min<int>(minw, (int)dt_width(l.dtype));
-  for (auto& op : R.outputs)
-    if (full(op.first) || flat) minw = std::min<int>(minw, (int)dt_width(node(op.first).dtype));
+  // A line region's V and TPL fix the order its reductions add in, so they depend only on what
+  // the reduced values are computed from (leaves, line length, the region's structure), never
+  // on which values are stored: a node evaluated alone and within eval_many over several roots
+  // then gets the same bits (kurumi_core/tests/engine.rs:224-243). Flat regions (no reductions)
+  // size their vectors by their outputs too.
+  if (flat)
+    for (auto& op : R.outputs) minw = std::min<int>(minw, (int)dt_width(node(op.first).dtype));
   V = contiguous_axis ? std::min(8, 16 / std::max(minw, 1)) : 1;
   while (V > 1 && (L % (uint64_t)V) != 0) V /= 2;
   leaf_vec.assign(R.leaves.size(), false);
@@ -468,9 +473,11 @@ void Gen::plan_layout() {
   // [8192, 4096] rmsnorm 5.76 -> 5.92 TB/s with 512 threads per row. Lines of 2-byte elements take 256 threads: the bf16 softmax rows (16 chunks each)
   // lose 3-4 % with 512, the bf16 [8192, 4096] rmsnorm rows run at 5.65 TB/s with 32 threads (16
   // chunks each) and 6.79 TB/s with 256 (2 each). Other widths: ~16 chunks per thread.
-  bool full_out = false;  // the line program stores a full-size output (a normalisation, softmax)
-  for (auto& op : R.outputs)
-    if (full(op.first)) full_out = true;
+  // a normalisation (softmax, rmsnorm): a full-size value computed from a line reduction; such
+  // regions usually store it, and store-heavy lines want more threads
+  bool full_out = false;
+  for (size_t i = 0; i < R.nodes.size(); ++i)
+    if (full((int)i) && R.nodes[i].level >= 1) full_out = true;
   int target = V == 4 ? (full_out ? 2 : 8) : V == 8 ? (int)std::max<uint64_t>(1, (chunks + 255) / 256) : 16;
   if (const char* e = std::getenv("KURUMI_HIP_LINE_CHUNKS")) target = std::max(1, std::atoi(e));
   uint64_t t = 1;

@@ -454,7 +454,6 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 bool gemm_lds_ok(const GemmArgs& a) {
   if (const char* e = std::getenv("KURUMI_HIP_NO_MFMA"); e && *e && *e != '0') return false;
-  if (const char* e = std::getenv("KURUMI_HIP_GEMM_V1"); e && *e && *e != '0') return false;
   const bool fp8 = a.in_type == GT_F8E4M3;
   if (!(a.in_type == GT_BF16 || a.in_type == GT_F16 || fp8)) return false;
   if (!(a.out_type == GT_BF16 || a.out_type == GT_F16 || a.out_type == GT_F32)) return false;
@@ -471,6 +470,14 @@ bool gemm_lds_ok(const GemmArgs& a) {
   }
   if (a.a && (!aligned16(a.a) || !aligned16(a.b))) return false;
   return a.batch <= 65535;
+}
+
+std::string gemm_lds_name(const GemmArgs& a) {
+  std::string n = a.in_type == GT_F8E4M3 ? "gemm_mfma_e4m3" : a.in_type == GT_F16 ? "gemm_mfma_f16" : "gemm_mfma_bf16";
+  n += a.sbk == 1 ? "_nt" : "_nn";
+  n += rows192(a) ? "_192x256" : "_256x256";
+  if (!spans_fit(a)) n += "_a64";
+  return n;
 }
 
 void launch_gemm_lds(const GemmArgs& a, hipStream_t s) {

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <string>
 
 namespace ku::hipbk {
 
@@ -28,8 +29,10 @@ struct GemmArgs {
   int round_type = -1;
 };
 
-// Returns a short name of the kernel variant that will run (for plan labels).
-const char* gemm_variant(const GemmArgs& a);
+// Short name of the kernel variant that will run (for plan labels): the MFMA kernel's element
+// type, layout and tile ("gemm_mfma_bf16_nn_256x256"; "_a64" when an operand spans 2^31 bytes or
+// more and the 64-bit-address DMA form runs), or "gemm_generic".
+std::string gemm_variant(const GemmArgs& a);
 void launch_gemm(const GemmArgs& a, hipStream_t s);
 
 struct AttnArgs {

@@ -1,6 +1,8 @@
 // Fusion planner + plan executor for the HIP backend (see plan.h).
 #include "plan.h"
 
+#include "fingerprint.h"
+
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
@@ -195,31 +197,76 @@ static bool view_eq(const View& a, const View& b) {
 
 // ======================= const cache =======================
 
-DevBuf ConstCache::get(const Graph& g, NodeId id) {
-  auto key = std::make_pair(g.id(), id);
-  auto it = map_.find(key);
-  if (it != map_.end()) return it->second;
-  const Node& n = g.node(id);
-  DevBuf b = ctx_->pool().alloc(std::max<size_t>(n.op.data->size(), 1));
-  if (!n.op.data->empty())
-    KU_HIP(hipMemcpyAsync(b.ptr, n.op.data->data(), n.op.data->size(), hipMemcpyHostToDevice, ctx_->stream()));
-  map_[key] = b;
-  return b;
+ConstCache::ConstCache(Context* ctx) : ctx_(ctx) {
+  const char* e = std::getenv("KURUMI_HIP_CONST_CACHE_MB");
+  budget_ = (size_t)(e && *e ? std::strtoull(e, nullptr, 10) : 2048) << 20;
+  ctx_->pool().add_reclaimer([this] { return reclaim(); });
 }
 
-void ConstCache::drop_graph(uint64_t gid) {
-  for (auto it = map_.begin(); it != map_.end();) {
-    if (it->first.first == gid) {
-      ctx_->pool().release(it->second);
-      it = map_.erase(it);
+std::shared_ptr<ConstEntry> ConstCache::get(const Graph& g, NodeId id) {
+  const Node& n = g.node(id);
+  auto fast = by_node_.find({g.id(), id});
+  if (fast != by_node_.end()) {
+    auto it = by_content_.find(fast->second);
+    if (it != by_content_.end()) {
+      it->second->last_use = ++clock_;
+      return it->second;
+    }
+    by_node_.erase(fast);
+  }
+  Hash128 h = payload_hash(n.op.data);
+  const size_t nb = n.op.data ? n.op.data->size() : 0;
+  Key key{h.lo, h.hi, nb, (uint32_t)n.op.data_dtype, n.op.shape};
+  if (by_node_.size() > (1u << 16)) by_node_.clear();  // stale fast-path records of freed graphs
+  by_node_[{g.id(), id}] = key;
+  auto it = by_content_.find(key);
+  if (it != by_content_.end()) {
+    it->second->last_use = ++clock_;
+    return it->second;
+  }
+  auto e = std::make_shared<ConstEntry>();
+  e->buf = ctx_->pool().alloc(std::max<size_t>(nb, 1));
+  e->pool = &ctx_->pool();
+  e->nbytes = e->buf.bytes;
+  e->last_use = ++clock_;
+  if (nb) KU_HIP(hipMemcpyAsync(e->buf.ptr, n.op.data->data(), nb, hipMemcpyHostToDevice, ctx_->stream()));
+  uploads_++;
+  by_content_[key] = e;
+  enforce_budget();
+  return e;
+}
+
+void ConstCache::enforce_budget() {
+  size_t idle = 0;
+  for (auto& kv : by_content_)
+    if (kv.second.use_count() == 1) idle += kv.second->nbytes;
+  while (idle > budget_) {
+    auto victim = by_content_.end();
+    for (auto it = by_content_.begin(); it != by_content_.end(); ++it)
+      if (it->second.use_count() == 1 && (victim == by_content_.end() || it->second->last_use < victim->second->last_use))
+        victim = it;
+    if (victim == by_content_.end()) break;
+    idle -= victim->second->nbytes;
+    by_content_.erase(victim);
+  }
+}
+
+size_t ConstCache::reclaim() {
+  size_t freed = 0;
+  for (auto it = by_content_.begin(); it != by_content_.end();) {
+    if (it->second.use_count() == 1) {
+      freed += it->second->nbytes;
+      it = by_content_.erase(it);
     } else {
       ++it;
     }
   }
+  return freed;
 }
 
 ConstCache::~ConstCache() {
-  for (auto& kv : map_) ctx_->pool().release(kv.second);
+  ctx_->pool().clear_reclaimers();
+  by_content_.clear();
 }
 
 // ======================= planner =======================
@@ -287,7 +334,7 @@ bool const_uniform_value(const Node& n, double* out) {
 
 class Planner {
  public:
-  Planner(Plan& P, ConstCache* consts) : P_(P), g_(P.g_), consts_(consts) {}
+  Planner(Plan& P, ConstCache* consts) : P_(P), g_(*P.bg_), consts_(consts) {}
   void run();
 
  private:
@@ -1239,33 +1286,50 @@ bool Planner::match_fp8_epilogue(NodeId castn) {
   auto single = [&](NodeId x) { return consumers_[x] == 1 && !root_set_.count(x); };
   NodeId m2 = cn.src[0];
   if (g_.node(m2).op.kind != OpKind::Mul || !single(m2)) return false;
-  auto bcast_src = [&](NodeId e, Shape* src_shape) -> long {
+  // e = Expand(Reshape(v, rs), es): the broadcast of a scale vector v. The reshape target rs
+  // decides which output axis v runs along, so it is returned for the caller to check (a
+  // per-row [M] scale reshaped to [M, 1] must never be taken for a per-column one, even when
+  // M == N and the source shapes agree).
+  struct Bcast { NodeId v; Shape rs, es; };
+  auto bcast_src = [&](NodeId e, Bcast* b) -> bool {
     const Node& en = g_.node(e);
-    if (en.op.kind != OpKind::Expand || !single(e)) return -1;
+    if (en.op.kind != OpKind::Expand || !single(e)) return false;
     const Node& rn = g_.node(en.src[0]);
-    if (rn.op.kind != OpKind::Reshape || !single(en.src[0])) return -1;
-    *src_shape = g_.shape(rn.src[0]);
-    return (long)rn.src[0];
+    if (rn.op.kind != OpKind::Reshape || !single(en.src[0])) return false;
+    *b = Bcast{rn.src[0], rn.shape, en.shape};
+    return true;
   };
-  auto split = [&](NodeId mul, NodeId* other, NodeId* vec, Shape* vs) {
+  // mul = other * bcast(v) (either operand order) with `ok` accepting the broadcast
+  auto split = [&](NodeId mul, NodeId* other, Bcast* b, const std::function<bool(const Bcast&)>& ok) {
     const Node& mn = g_.node(mul);
     for (int t = 0; t < 2; ++t) {
-      long s = bcast_src(mn.src[1 - t], vs);
-      if (s >= 0) { *other = mn.src[t]; *vec = (NodeId)s; return true; }
+      Bcast c;
+      if (bcast_src(mn.src[1 - t], &c) && ok(c)) { *other = mn.src[t]; *b = c; return true; }
     }
     return false;
   };
-  NodeId m1, sw, sx, dot;
-  Shape sws, sxs;
-  if (!split(m2, &m1, &sw, &sws)) return false;
+  const Shape& ys = g_.shape(m2);
+  if (ys.size() != 2) return false;
+  const size_t M = ys[0], N = ys[1];
+  // per-column weight scale: sw [N] or [1, N] -> [1, N] -> [M, N]
+  auto col_scale = [&](const Bcast& b) {
+    const Shape& vs = g_.shape(b.v);
+    return b.rs == Shape{1, N} && b.es == Shape{M, N} && (vs == Shape{N} || vs == Shape{1, N}) &&
+           g_.dtype(b.v) == DType::F32;
+  };
+  // per-tensor activation scale: one element -> [1, 1] -> [M, N]
+  auto tensor_scale = [&](const Bcast& b) {
+    return b.rs == Shape{1, 1} && b.es == Shape{M, N} && numel(g_.shape(b.v)) == 1 && g_.dtype(b.v) == DType::F32;
+  };
+  NodeId m1, dot;
+  Bcast swb, sxb;
+  if (!split(m2, &m1, &swb, col_scale)) return false;
   if (g_.node(m1).op.kind != OpKind::Mul || !single(m1)) return false;
-  if (!split(m1, &dot, &sx, &sxs)) return false;
+  if (!split(m1, &dot, &sxb, tensor_scale)) return false;
+  const NodeId sw = swb.v, sx = sxb.v;
   const Node& dn = g_.node(dot);
-  if (dn.op.kind != OpKind::DotGeneral || !single(dot) || dn.shape.size() != 2) return false;
+  if (dn.op.kind != OpKind::DotGeneral || !single(dot) || dn.shape != (Shape{M, N})) return false;
   if (dn.op.lc != std::vector<size_t>{1} || dn.op.rc != std::vector<size_t>{1} || !dn.op.lb.empty()) return false;
-  size_t N = dn.shape[1];
-  if (numel(sxs) != 1 || g_.dtype(sx) != DType::F32) return false;
-  if (!(sws == Shape{N} || sws == Shape{1, N}) || g_.dtype(sw) != DType::F32) return false;
   if (dn.dtype != DType::F32) return false;
   NodeId ca = dn.src[0], cb = dn.src[1];
   const Node &can = g_.node(ca), &cbn = g_.node(cb);
@@ -1477,19 +1541,23 @@ void Planner::run() {
 static bool debug_enabled();
 
 Plan::Plan(const Graph& g, const std::vector<NodeId>& roots, Context* ctx, ConstCache* consts)
-    : g_(g), graph_id_(g.id()), roots_(roots), ctx_(ctx) {
+    : bg_(&g), roots_(roots), ctx_(ctx) {
   if (roots.empty()) throw Error("eval: no output nodes");
   Planner pl(*this, consts);
   pl.run();
+  for (auto& kv : input_slots_) input_meta_[kv.first] = {g.dtype(kv.first), g.shape(kv.first)};
+  for (NodeId r : roots_) root_meta_.push_back({g.dtype(r), g.shape(r)});
   compile();
   if (ctx_) {
     allocate();
     for (auto& s : slots_)
       if (s.kind == SlotKind::Const) {
-        s.buf = consts->get(g, s.node);
+        const_refs_.push_back(consts->get(g, s.node));
+        s.buf = const_refs_.back()->buf;
         s.borrowed = true;
       }
   }
+  bg_ = nullptr;
 }
 
 Plan::~Plan() {
@@ -1555,10 +1623,10 @@ std::vector<NodeId> Plan::inputs() const {
 void Plan::feed(NodeId input, const Tensor& t) {
   auto it = input_slots_.find(input);
   if (it == input_slots_.end()) return;  // not reachable from the roots
-  const Node& n = g_.node(input);
-  if (t.dtype != n.dtype || t.shape != n.shape)
+  const auto& meta = input_meta_.at(input);
+  if (t.dtype != meta.first || t.shape != meta.second)
     throw Error("feed for input %" + std::to_string(input) + ": got " + dt_name(t.dtype) + shape_str(t.shape) +
-                ", expected " + dt_name(n.dtype) + shape_str(n.shape));
+                ", expected " + dt_name(meta.first) + shape_str(meta.second));
   Slot& s = slots_[it->second];
   if (t.bytes.size() != s.bytes) throw Error("feed: byte size mismatch");
   if (!s.bytes) return;
@@ -1689,10 +1757,9 @@ void* Plan::output_ptr(size_t i) const { return slots_[root_vals_.at(i).first].b
 
 Tensor Plan::download(size_t i) {
   const auto& rv = root_vals_.at(i);
-  NodeId r = roots_.at(i);
   Tensor t;
-  t.dtype = g_.dtype(r);
-  t.shape = g_.shape(r);
+  t.dtype = root_meta_.at(i).first;
+  t.shape = root_meta_.at(i).second;
   t.bytes.resize(numel(t.shape) * dt_width(t.dtype));
   if (!t.bytes.empty())
     KU_HIP(hipMemcpyAsync(t.bytes.data(), slots_[rv.first].buf.ptr, t.bytes.size(), hipMemcpyDeviceToHost,

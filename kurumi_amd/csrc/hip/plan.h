@@ -149,6 +149,18 @@ struct Step {
   std::string label;
 };
 
+// One uploaded constant. Plans hold it through a shared_ptr, so a buffer is returned to the
+// pool only once neither the cache nor any plan uses it.
+struct ConstEntry {
+  Pool* pool = nullptr;
+  DevBuf buf;
+  size_t nbytes = 0;
+  uint64_t last_use = 0;
+  ~ConstEntry() {
+    if (pool) pool->release(buf);
+  }
+};
+
 class Backend;  // HipBackend (backend.h)
 
 class Plan {
@@ -181,9 +193,13 @@ class Plan {
   void allocate();
   void launch_step(const Step& s);
 
-  const Graph& g_;
-  uint64_t graph_id_;
+  const Graph* bg_ = nullptr;  // the graph being planned; valid during construction only
   std::vector<NodeId> roots_;
+  // what feed() and download() check against, so a built plan never reads its graph again
+  // (a content-equal graph may reuse it after the original is freed)
+  std::map<NodeId, std::pair<DType, Shape>> input_meta_;
+  std::vector<std::pair<DType, Shape>> root_meta_;
+  std::vector<std::shared_ptr<ConstEntry>> const_refs_;
   Context* ctx_;
   std::vector<Slot> slots_;
   std::vector<Region> regions_;
@@ -199,18 +215,42 @@ class Plan {
   hipGraphExec_t hexec_ = nullptr;
 };
 
-// Backend-owned cache of uploaded constants keyed by (graph id, node)
-// (kurumi_metal/src/backend.rs:23-26, eval_walk.rs:99-114).
+// Backend-owned cache of uploaded constants (kurumi_metal/src/backend.rs:23-26,
+// eval_walk.rs:99-114 key theirs by graph id and node). Here the key is the payload's content
+// (dtype, shape, byte count and a 128-bit hash of the bytes), with (graph id, node) as a fast
+// path, so a graph rebuilt with the same weights reuses their device copies. Entries that no
+// live plan holds are kept up to a byte budget (KURUMI_HIP_CONST_CACHE_MB, default 2048),
+// least recently used first out, and all of them are dropped when an allocation fails.
 class ConstCache {
  public:
-  explicit ConstCache(Context* ctx) : ctx_(ctx) {}
+  explicit ConstCache(Context* ctx);
   ~ConstCache();
-  DevBuf get(const Graph& g, NodeId id);
-  void drop_graph(uint64_t gid);
+  std::shared_ptr<ConstEntry> get(const Graph& g, NodeId id);
+  // Drop every entry no plan holds; returns the bytes released.
+  size_t reclaim();
+  size_t entries() const { return by_content_.size(); }
+  size_t uploads() const { return uploads_; }
 
  private:
+  struct Key {
+    uint64_t h0, h1, nbytes;
+    uint32_t dtype;
+    Shape shape;
+    bool operator<(const Key& o) const {
+      if (h0 != o.h0) return h0 < o.h0;
+      if (h1 != o.h1) return h1 < o.h1;
+      if (nbytes != o.nbytes) return nbytes < o.nbytes;
+      if (dtype != o.dtype) return dtype < o.dtype;
+      return shape < o.shape;
+    }
+  };
+  void enforce_budget();
   Context* ctx_;
-  std::map<std::pair<uint64_t, NodeId>, DevBuf> map_;
+  std::map<Key, std::shared_ptr<ConstEntry>> by_content_;
+  std::map<std::pair<uint64_t, NodeId>, Key> by_node_;
+  uint64_t clock_ = 0;
+  size_t uploads_ = 0;
+  size_t budget_;
 };
 
 // Generated-source entry points (codegen.cpp)

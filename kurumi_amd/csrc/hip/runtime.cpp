@@ -45,8 +45,9 @@ DevBuf Pool::alloc(size_t bytes) {
   void* p = nullptr;
   hipError_t e = hipMalloc(&p, b);
   if (e != hipSuccess) {
-    // release cached buffers and retry once
+    // return reclaimable buffers, release everything cached and retry once
     (void)hipGetLastError();
+    for (auto& r : reclaimers_) r();
     trim();
     KU_HIP(hipMalloc(&p, b));
   }

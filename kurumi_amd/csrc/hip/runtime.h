@@ -10,6 +10,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include <cstdint>
+#include <functional>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -39,9 +40,14 @@ class Pool {
   void trim();
   size_t bytes_live() const { return live_; }
   size_t bytes_cached() const { return cached_; }
+  // Called when hipMalloc fails, before the retry: each returns buffers it held to the pool
+  // (e.g. cached constants that no plan uses) so the trim can free them.
+  void add_reclaimer(std::function<size_t()> f) { reclaimers_.push_back(std::move(f)); }
+  void clear_reclaimers() { reclaimers_.clear(); }
 
  private:
   static size_t bucket(size_t bytes);
+  std::vector<std::function<size_t()>> reclaimers_;
   std::multimap<size_t, void*> free_;
   size_t live_ = 0, cached_ = 0;
 };

@@ -7,7 +7,8 @@
 //
 //   sx = reduce_max(reduce_max(|x|, 1), 0) * (1/448)        (per-tensor, in-graph)
 //   xq = cast_e4m3(x * (1/sx))
-//   sw[n] = max_k |w[n,k]| / 448, wq = cast_e4m3(w / sw[n])  (per row; host-side when w is a Const)
+//   sw[n] = max_k |w[n,k]| / 448, wq = cast_e4m3(w / sw[n])  (per row; host-side when w is a Const,
+//                                                            from the stored f32 weight)
 //   y  = cast_out( dot(cast_f32(xq), cast_f32(wq)) * sx * sw[n] )
 //
 // whose device lowering is one fp8 MFMA GEMM with the scales in its epilogue. The
@@ -51,15 +52,16 @@ bool is_linear(const Graph& g, NodeId id) {
 
 }  // namespace
 
-// Host values of a constant weight: a float Const, or a Cast{f32|bf16|f16} of one (the cast is
-// folded with its rounding). False for anything else.
+// Host values of a constant weight: a float Const, or a Cast{f32|bf16|f16} of one. A narrowing
+// cast is looked through: the e4m3 policy quantizes the stored weight itself (one rounding,
+// straight to e4m3 with its per-row scale) rather than a 16-bit rounding of it, which would
+// round twice. False for anything else.
 bool const_weight_f32(const Graph& g, NodeId w, std::vector<float>* out) {
   const Node& n = g.node(w);
-  DType round_to = DType::F32;
   const Node* c = &n;
   if (n.op.kind == OpKind::Cast) {
-    round_to = n.op.to;
-    if (round_to != DType::F32 && round_to != DType::BF16 && round_to != DType::F16) return false;
+    DType to = n.op.to;
+    if (to != DType::F32 && to != DType::BF16 && to != DType::F16) return false;
     c = &g.node(n.src[0]);
   }
   if (c->op.kind != OpKind::Const) return false;
@@ -68,12 +70,7 @@ bool const_weight_f32(const Graph& g, NodeId w, std::vector<float>* out) {
   size_t cnt = numel(c->op.shape), wd = dt_width(dt);
   const uint8_t* p = c->op.data->data();
   out->resize(cnt);
-  for (size_t i = 0; i < cnt; ++i) {
-    double v = load_as_f64(dt, p + i * wd);
-    if (round_to == DType::BF16) v = bf16_to_f32(f64_to_bf16(v));
-    else if (round_to == DType::F16) v = f16_to_f64(f64_to_f16(v));
-    (*out)[i] = static_cast<float>(v);
-  }
+  for (size_t i = 0; i < cnt; ++i) (*out)[i] = static_cast<float>(load_as_f64(dt, p + i * wd));
   return true;
 }
 

@@ -51,17 +51,28 @@ def test_cfg2_single_kernel_for_softmax_and_argmax(dt, decomposed):
 def test_cfg3_gemm_steps():
     g = Graph()
     c = g.matmul(g.input([4096, 4096], DType.BF16), g.input([4096, 11008], DType.BF16))
-    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn b1 m4096 n11008 k4096"]
+    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn_256x256 b1 m4096 n11008 k4096"]
     g = Graph()
     c = g.dot_general(g.input([8, 2048, 128], DType.BF16), g.input([8, 128, 2048], DType.BF16), [2], [1], [0], [0])
-    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn b8 m2048 n2048 k128"]
+    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn_256x256 b8 m2048 n2048 k128"]
     g = Graph()
     c = g.dot_general(g.input([64, 256], DType.BF16), g.input([128, 256], DType.BF16), [1], [1])
-    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nt b1 m64 n128 k256"]
+    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nt_192x256 b1 m64 n128 k256"]
     g = Graph()  # transposed lhs is canonicalised by a copy kernel first
     c = g.dot_general(g.input([256, 64], DType.BF16), g.input([256, 128], DType.BF16), [0], [0])
     st = steps(g.codegen([c], compile=True))
     assert len(st) == 2 and st[0].startswith("ku_ew") and st[1].startswith("gemm_mfma_bf16_nn")
+
+
+def test_gemm_labels_name_the_tile_and_the_64bit_form():
+    g = Graph()  # 2^31 bytes of A: the 64-bit-address DMA form
+    c = g.matmul(g.input([262144, 4096], DType.BF16), g.input([4096, 256], DType.BF16))
+    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn_256x256_a64 b1 m262144 n256 k4096"]
+    g = Graph()  # 256 tiles of 256 x 256 fill one round: 256-row tiles
+    x = g.input([4096, 512], DType.BF16)
+    w = g.constant(np.random.default_rng(0).normal(0, 0.02, (4096, 512)).astype(np.float32))
+    st = steps(g.codegen([K.amp_fp8(g, g.dot_general(x, g.cast(w, DType.BF16), [1], [1]))], compile=True))
+    assert st[-1] == "gemm_mfma_e4m3_nt_256x256 b1 m4096 n4096 k512"
 
 
 @pytest.mark.parametrize("fused", [True, False])
@@ -95,7 +106,7 @@ def test_cfg5_fp8_linear_lowering():
     assert g.dtype(y) == DType.BF16 and g.shape(y) == (2048, 256)
     st = steps(g.codegen([y], compile=True))
     # weights quantised on the host; on device: absmax rows, absmax, scale, quantise, fp8 GEMM
-    assert st[-1] == "gemm_mfma_e4m3_nt b1 m2048 n256 k4096"
+    assert st[-1] == "gemm_mfma_e4m3_nt_192x256 b1 m2048 n256 k4096"
     assert not any("256x4096" in s for s in st)
     assert len(st) <= 6
 
@@ -255,3 +266,29 @@ def test_multi_wave_lines_are_one_group_each(rows, cols, dt):
         assert lb == tpl, (lb, tpl)
     else:
         assert lb % tpl == 0
+
+
+def _scaled_fp8_dot(m, n, k, per_row: bool):
+    """cast(dot(f32(xq), f32(wq)) * bcast(sx) * bcast(s), bf16) with s a per-column [n] scale
+    (reshape [1, n]) or a per-row [m] scale (reshape [m, 1])."""
+    g = Graph()
+    xq = g.input([m, k], DType.F8E4M3)
+    wq = g.input([n, k], DType.F8E4M3)
+    sx = g.input([1], DType.F32)
+    s = g.input([m] if per_row else [n], DType.F32)
+    d = g.dot_general(g.cast(xq, DType.F32), g.cast(wq, DType.F32), [1], [1])
+    y1 = g.mul(d, g.expand(g.reshape(sx, [1, 1]), [m, n]))
+    y2 = g.mul(y1, g.expand(g.reshape(s, [m, 1] if per_row else [1, n]), [m, n]))
+    return g, (xq, wq, sx, s), g.cast(y2, DType.BF16)
+
+
+def test_fp8_epilogue_matcher_takes_column_scales_only():
+    # per-column scale: one fp8 GEMM with the scales in its epilogue
+    g, _, y = _scaled_fp8_dot(256, 256, 128, per_row=False)
+    st = steps(g.codegen([y], compile=True))
+    assert len(st) == 1 and st[0].startswith("gemm_mfma_e4m3_nt"), st
+    # a per-row scale on a square output has the same source shape but runs along the other
+    # axis: the matcher must decline it (no fp8 GEMM step)
+    g, _, y = _scaled_fp8_dot(256, 256, 128, per_row=True)
+    st = steps(g.codegen([y], compile=True))
+    assert not any(s.startswith("gemm_mfma_e4m3") for s in st), st

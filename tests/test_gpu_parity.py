@@ -280,6 +280,11 @@ def test_cfg5_fp8_linear_matches_dequant_f64(hip):
     want = to_f32(interpret(g, [y], feeds)[0])
     assert rel_err(got, want) <= 3e-2
     assert_close(got, want, rtol=3e-2, atol=3e-2 * np.abs(want).max(), what="fp8 vs oracle")
+    # and the stated oracle of the config: the dequantised-f64 product
+    from test_gpu_bench_configs import dequant_f64_linear
+
+    truth = dequant_f64_linear(f32_to_bf16_bits(xv), wv.astype(np.float32))
+    assert_close(got, truth, rtol=3e-2, atol=3e-2 * np.abs(truth).max(), what="fp8 vs dequantised f64")
 
 
 # ---------------- casts, ints, misc primitives (bit-exact) ----------------
@@ -364,12 +369,20 @@ def test_rmsnorm_and_column_reductions(hip):
     np.testing.assert_array_equal(got[2].numpy(), want[2].numpy())
 
 
-def test_eval_many_matches_single_eval(hip):
-    # backend.rs contract: eval_many shares one pass and equals per-node eval
-    g, x, y, a = softmax_graph(16, 1000, DType.F32, True)
-    feeds = {x: Tensor.from_numpy(randn([16, 1000], 91, 3.0))}
-    both = hip.eval_many_with(g, [y, a], feeds)
-    np.testing.assert_array_equal(both[1].numpy(), hip.eval_with(g, a, feeds).numpy())
+@pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
+def test_eval_many_matches_single_eval(hip, dt):
+    # backend.rs contract (kurumi_core/tests/engine.rs:228-243): eval_many shares one pass and
+    # equals per-node eval bit for bit, on every output
+    g, x, y, a = softmax_graph(16, 1000, dt, True)
+    s = g.sum(y, 1)
+    xv = randn([16, 1000], 91, 3.0)
+    feeds = {x: Tensor.from_numpy(xv) if dt == DType.F32 else bf16_tensor(xv)}
+    roots = [y, a, s, x]
+    many = hip.eval_many_with(g, roots, feeds)
+    for i, r in enumerate(roots):
+        one = hip.eval_with(g, r, feeds)
+        assert many[i].dtype == one.dtype and many[i].shape == one.shape
+        np.testing.assert_array_equal(many[i].numpy(), one.numpy(), err_msg=f"output {i}")
 
 
 def test_missing_feed_is_an_error(hip):
@@ -448,3 +461,21 @@ def test_argmax_over_an_empty_axis_is_an_error(hip):
     x = g.input([3, 0], DType.F32)
     with pytest.raises(KuError, match="empty axis"):
         hip.eval_with(g, g.argmax(x, 1), {x: Tensor.from_numpy(np.zeros((3, 0), np.float32))})
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+def test_scaled_fp8_dot_square_output_matches_oracle(hip, per_row):
+    """A square [m, m] output scaled per row must not be taken for the per-column fp8 epilogue."""
+    from test_codegen import _scaled_fp8_dot
+
+    m, k = 256, 128
+    g, (xq, wq, sx, s), y = _scaled_fp8_dot(m, m, k, per_row)
+    rng = np.random.default_rng(31)
+    xb = cast_bits(rng.standard_normal((m, k)).astype(np.float32) * 8, DType.F32, DType.F8E4M3)
+    wb = cast_bits(rng.standard_normal((m, k)).astype(np.float32) * 8, DType.F32, DType.F8E4M3)
+    feeds = {xq: Tensor(DType.F8E4M3, [m, k], xb.tobytes()), wq: Tensor(DType.F8E4M3, [m, k], wb.tobytes()),
+             sx: Tensor.from_numpy(np.array([0.01], np.float32)),
+             s: Tensor.from_numpy(np.linspace(0.5, 4.0, m).astype(np.float32))}
+    got = to_f32(hip.eval_with(g, y, feeds))
+    want = to_f32(interpret(g, [y], feeds)[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what=f"scaled fp8 dot per_row={per_row}")

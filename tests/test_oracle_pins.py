@@ -54,6 +54,26 @@ def test_randn_moments():
     assert abs(x.mean()) < 0.01 and abs(x.std() - 1.0) < 0.01
 
 
+@pytest.mark.parametrize("seed", [0, 9, 0xFFFF_FFFF_FFFF_FFFF])
+def test_randn_is_box_muller_over_the_two_pinned_streams(seed):
+    """graph/ops/core/random.rs:28-40: sqrt(-2 ln max(u1, 1e-7)) * cos(2 pi u2), u1 from `seed`
+    and u2 from `seed ^ 0xD1B5_4A32_D192_ED03`, each the KAT-pinned uniform map. Recomputed
+    here in f64 from those uniforms; the oracle's f32 primitive chain (ln through log2, cos as
+    sin(x + pi/2)) stays within a few f32 ulps of it. A wrong stream constant, a swapped branch
+    (sin) or a dropped clamp fails."""
+    from kutest import rand_uniform, randn
+
+    n = 50000
+    x = randn([n], seed).astype(np.float64)
+    u1 = rand_uniform(seed, n).astype(np.float64)
+    u2 = rand_uniform(seed ^ 0xD1B54A32D192ED03, n).astype(np.float64)
+    want = np.sqrt(-2.0 * np.log(np.maximum(u1, np.float64(np.float32(1e-7))))) * np.cos(2.0 * np.pi * u2)
+    err = np.abs(x - want)
+    assert (err <= 4e-6 * np.maximum(1.0, np.abs(want))).all(), err.max()
+    # the clamp binds exactly where the first stream is below 1e-7
+    assert np.abs(want).max() < 5.7
+
+
 # ---------------- conversions ----------------
 
 def test_bf16_round_trip_exhaustive_and_ties():
