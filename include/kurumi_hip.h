@@ -257,6 +257,18 @@ void ku_hip_plan_free(KuHipPlan *p);
  * compile != 0). Returns the byte length; copies at most cap bytes into out. */
 size_t ku_hip_codegen(KuGraph *g, const KuNode *roots, size_t n, uint32_t compile, uint8_t *out, size_t cap);
 
+/* The e4m3 linear layer on caller-owned device buffers, the graph ku_amp_fp8 emits for one
+ * layer as one call: sx = max|x| / 448 (computed on the device), xq = e4m3(x / sx) and
+ * y = (xq @ wq^T) * sx * sw[n] rounded to y_dtype, on the fp8 MFMA GEMM.
+ *   x  [m, k] KU_BF16 / KU_F16 / KU_F32, wq [n, k] KU_F8E4M3 (e.g. rows quantised with per-row
+ *   absmax / 448 scales sw [n] f32), y [m, n] KU_BF16 / KU_F16 / KU_F32; all row-major, 16-byte
+ *   aligned device pointers; k a multiple of 128.
+ * Enqueued on `stream` (a hipStream_t; NULL = the backend's stream), asynchronously. Scratch (the
+ * quantised activation, m*k bytes) is a workspace of the backend that grows on demand, so calls
+ * on one backend must be ordered on one stream. Returns 0, or -1 with ku_last_error. */
+int32_t ku_hip_linear_e4m3(const KuBackend *b, const void *x, uint32_t x_dtype, const uint8_t *wq, const float *sw,
+                           void *y, uint32_t y_dtype, size_t m, size_t n, size_t k, void *stream);
+
 /* Counters of a backend into out[0..cap): launches per kind (fused, gemm, attention, upload,
  * download), then plans built, constants uploaded and constants cached (plans and constants
  * are cached by graph content, so an equal graph rebuilt per call adds to neither); returns

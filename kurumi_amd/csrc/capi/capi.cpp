@@ -11,6 +11,7 @@
 
 #include "../../../include/kurumi_hip.h"
 #include "../hip/backend.h"
+#include "../hip/kernels/kernels.h"
 #include "errors.h"
 #include "handles.h"
 #include "../ir/graph.h"
@@ -633,6 +634,36 @@ size_t ku_hip_codegen(KuGraph* g, const KuNode* roots, size_t n, uint32_t compil
     for (size_t i = 0; i < plan.num_steps(); ++i) all += "// step " + std::to_string(i) + ": " + plan.step_label(i) + "\n";
     if (out && cap) std::memcpy(out, all.data(), std::min(cap, all.size()));
     return all.size();
+  });
+}
+
+int32_t ku_hip_linear_e4m3(const KuBackend* b, const void* x, uint32_t x_dtype, const uint8_t* wq, const float* sw,
+                           void* y, uint32_t y_dtype, size_t m, size_t n, size_t k, void* stream) {
+  if (!b) {
+    set_err("ku_hip_linear_e4m3: null backend handle");
+    return -1;
+  }
+  return guard<int32_t>(-1, [&] {
+    ku::hipbk::LinearE4m3Args a;
+    a.x = x;
+    a.x_type = (int)x_dtype;
+    a.wq = wq;
+    a.sw = sw;
+    a.y = y;
+    a.y_type = (int)y_dtype;
+    a.m = (int64_t)m;
+    a.n = (int64_t)n;
+    a.k = (int64_t)k;
+    auto& ctx = b->b->ctx();
+    ctx.make_current();
+    const size_t need = ku::hipbk::linear_e4m3_scratch_bytes(a.m, a.k);
+    void* ws = b->b->workspace(need);
+    try {
+      ku::hipbk::linear_e4m3(a, ws, need, stream ? static_cast<hipStream_t>(stream) : ctx.stream());
+    } catch (const std::runtime_error& e) {
+      throw ku::Error(std::string("ku_hip_linear_e4m3: ") + e.what());
+    }
+    return 0;
   });
 }
 

@@ -12,6 +12,10 @@ HipBackend::HipBackend(int device) {
 }
 
 HipBackend::~HipBackend() {
+  if (ws_.ptr) {
+    (void)hipDeviceSynchronize();
+    ctx_->pool().release(ws_);
+  }
   plans_.clear();
   consts_.reset();
   ctx_.reset();
@@ -44,6 +48,19 @@ std::shared_ptr<Plan> HipBackend::plan_for(const Graph& g, const std::vector<Nod
   plans_.push_front(Entry{g.id(), g.size(), roots, fp, p});
   while (plans_.size() > kMaxCachedPlans) plans_.pop_back();
   return p;
+}
+
+void* HipBackend::workspace(size_t bytes) {
+  if (ws_.ptr && ws_.bytes >= bytes) return ws_.ptr;
+  ctx_->make_current();
+  if (ws_.ptr) {
+    // kernels of earlier calls (on whatever stream the caller gave) may still read the old one
+    KU_HIP(hipDeviceSynchronize());
+    ctx_->pool().release(ws_);
+    ws_ = DevBuf{};
+  }
+  ws_ = ctx_->pool().alloc(bytes);
+  return ws_.ptr;
 }
 
 void feed_plan(Plan& p, const Feeds& feeds) {

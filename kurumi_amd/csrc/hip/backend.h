@@ -27,6 +27,9 @@ class HipBackend : public ku::Backend {
   size_t plans_built() const { return plans_built_; }
   std::unique_ptr<Plan> new_plan(const Graph& g, const std::vector<NodeId>& roots);
   Context& ctx() { return *ctx_; }
+  // Grow-only device workspace of the direct kernel entry points (ku_hip_linear_e4m3): at least
+  // `bytes`, reused by every call on this backend (calls must be ordered on one stream).
+  void* workspace(size_t bytes);
   ConstCache& consts() { return *consts_; }
 
  private:
@@ -40,6 +43,7 @@ class HipBackend : public ku::Backend {
     std::shared_ptr<Plan> plan;
   };
   std::list<Entry> plans_;  // most recent first
+  DevBuf ws_;
   size_t plans_built_ = 0;
 };
 

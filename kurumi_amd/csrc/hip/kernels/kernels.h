@@ -70,4 +70,34 @@ void launch_quant_dequant(const QuantArgs& a, hipStream_t s);
 bool quant_mm_ok(const QuantArgs& a);
 void launch_quant_mm(const QuantArgs& a, hipStream_t s);
 
+// Per-tensor e4m3 activation quantisation (linear_e4m3.hip): sx = max|x| * (1/448) and
+// xq = e4m3(x * (1/sx)) over n contiguous elements, in two kernels (absmax partials, then fold
+// + quantise). `partials` holds actq_partials_bytes(n) bytes of scratch.
+constexpr int kActqMaxPartials = 1024;
+struct ActQArgs {
+  const void* x = nullptr;  // [n] bf16 / f16 / f32, 16-byte aligned
+  int x_type = GT_BF16;
+  int64_t n = 0;
+  uint8_t* xq = nullptr;    // [n] e4m3
+  float* sx = nullptr;      // [1]
+  float* partials = nullptr;
+};
+size_t actq_partials_bytes(int64_t n);
+void launch_actq(const ActQArgs& a, hipStream_t s);
+
+// The e4m3 linear on device buffers: y[M, N] = round_y((e4m3(x / sx) @ wq^T) * sx * sw[n]) with
+// sx = max|x| / 448 computed on the device (the graph ku_amp_fp8 emits for one linear layer).
+struct LinearE4m3Args {
+  const void* x = nullptr;     // [M, K] row-major, x_type
+  int x_type = GT_BF16;
+  const uint8_t* wq = nullptr; // [N, K] e4m3 row-major
+  const float* sw = nullptr;   // [N] per-row weight scales
+  void* y = nullptr;           // [M, N] row-major, y_type
+  int y_type = GT_BF16;
+  int64_t m = 0, n = 0, k = 0;
+};
+// bytes of scratch one call needs: absmax partials, sx and the quantised activation (M*K)
+size_t linear_e4m3_scratch_bytes(int64_t m, int64_t k);
+void linear_e4m3(const LinearE4m3Args& a, void* scratch, size_t scratch_bytes, hipStream_t s);
+
 }  // namespace ku::hipbk

@@ -400,9 +400,12 @@ class Planner {
   bool match_attention(NodeId d2);
   bool match_fp8_epilogue(NodeId castn);
   bool match_cast_epilogue(NodeId castn);
+  bool match_actq(NodeId xq, NodeId sx);
+  void visit_actq(NodeId sx);
 
   struct AttnPattern { NodeId q, k, v; float scale; bool causal; };
   struct Fp8Pattern { NodeId dot, xq, wq, sx, sw; };
+  struct ActqPattern { NodeId x, xq; };
 
   Plan& P_;
   const Graph& g_;
@@ -413,6 +416,8 @@ class Planner {
   std::map<NodeId, AttnPattern> attn_pat_;
   std::map<NodeId, Fp8Pattern> fp8_pat_;
   std::map<NodeId, NodeId> cast_pat_;  // dot -> the cast its GEMM epilogue performs
+  std::map<NodeId, ActqPattern> actq_pat_;  // sx -> the activation quantisation producing it
+  std::vector<std::vector<NodeId>> users_;
   std::vector<int> region_step_;
   std::vector<int> slot_producer_;
   std::vector<bool> step_alive_;
@@ -1358,6 +1363,130 @@ bool Planner::match_fp8_epilogue(NodeId castn) {
   return true;
 }
 
+// The activation half of the e4m3 linear (the chain the e4m3 pass emits, ir/pass_fp8.cpp):
+//   xa = max(xf, neg(xf)), am = reduce_max(reduce_max(xa, 1), 0), sx = am * (1/448),
+//   xq = cast_e4m3(xf2 * expand(reshape(recip(sx), [1, 1]), [M, K]))
+// with xf, xf2 = x or cast_f32(x) and x a bf16 / f16 / f32 [M, K] value. It becomes one ACTQ step
+// (two kernels) producing xq and sx, in place of three generated kernels. Every absorbed node
+// must be used only inside the chain (sx and xq may have other users: they are materialised).
+bool Planner::match_actq(NodeId xq, NodeId sx) {
+  auto kind = [&](NodeId n) { return g_.node(n).op.kind; };
+  const Node& qn = g_.node(xq);
+  if (qn.op.kind != OpKind::Cast || qn.dtype != DType::F8E4M3 || absorbed_[xq]) return false;
+  const NodeId mul = qn.src[0];
+  if (kind(mul) != OpKind::Mul) return false;
+  // one operand is the broadcast reciprocal of sx, the other x as f32
+  NodeId inv = 0, invr = 0, invb = 0, xf2 = 0;
+  bool found = false;
+  for (int t = 0; t < 2 && !found; ++t) {
+    const NodeId e = g_.node(mul).src[t];
+    if (kind(e) != OpKind::Expand) continue;
+    const NodeId r = g_.node(e).src[0];
+    if (kind(r) != OpKind::Reshape || g_.shape(r) != Shape{1, 1}) continue;
+    const NodeId i = g_.node(r).src[0];
+    if (kind(i) != OpKind::Recip || g_.node(i).src[0] != sx) continue;
+    inv = i; invr = r; invb = e; xf2 = g_.node(mul).src[1 - t];
+    found = true;
+  }
+  if (!found) return false;
+  auto source_of = [&](NodeId f) -> NodeId {  // x for f = x (f32) or f = cast_f32(x)
+    if (g_.dtype(f) != DType::F32) return Graph::kNoNode;
+    if (kind(f) == OpKind::Cast) {
+      NodeId x = g_.node(f).src[0];
+      DType d = g_.dtype(x);
+      return d == DType::BF16 || d == DType::F16 ? x : Graph::kNoNode;
+    }
+    return f;
+  };
+  const NodeId x = source_of(xf2);
+  if (x == Graph::kNoNode) return false;
+  const Shape& xs = g_.shape(x);
+  if (xs.size() != 2 || g_.shape(invb) != xs || numel(xs) == 0) return false;
+  // sx = am * (1/448)
+  const Node& sn = g_.node(sx);
+  if (sn.op.kind != OpKind::Mul || sn.dtype != DType::F32 || numel(sn.shape) != 1) return false;
+  NodeId am = 0, sc = 0;
+  found = false;
+  for (int t = 0; t < 2 && !found; ++t) {
+    NodeId c = sn.src[1 - t], cst = c;
+    if (kind(c) == OpKind::Expand) cst = g_.node(c).src[0];
+    double v;
+    if (!const_uniform_value(g_.node(cst), &v) || g_.node(cst).op.data_dtype != DType::F32 ||
+        (float)v != 1.0f / 448.0f)
+      continue;
+    am = sn.src[t];
+    sc = c;
+    found = true;
+  }
+  if (!found) return false;
+  const Node& amn = g_.node(am);
+  if (amn.op.kind != OpKind::ReduceMax || amn.op.axis != 0) return false;
+  const NodeId rm = amn.src[0];
+  const Node& rmn = g_.node(rm);
+  if (rmn.op.kind != OpKind::ReduceMax || rmn.op.axis != 1 || g_.shape(rm) != Shape{xs[0]}) return false;
+  const NodeId xa = rmn.src[0];
+  const Node& xan = g_.node(xa);
+  if (xan.op.kind != OpKind::Max) return false;
+  NodeId xf = 0, ng = 0;
+  found = false;
+  for (int t = 0; t < 2 && !found; ++t) {
+    NodeId a = xan.src[t], b = xan.src[1 - t];
+    if (kind(b) == OpKind::Neg && g_.node(b).src[0] == a && source_of(a) == x) {
+      xf = a; ng = b;
+      found = true;
+    }
+  }
+  if (!found) return false;
+  // every absorbed node is used only by nodes of the chain
+  std::set<NodeId> chain = {xa, ng, rm, am, inv, invr, invb, mul, sc, xq, sx};
+  if (xf != x) chain.insert(xf);
+  if (xf2 != x) chain.insert(xf2);
+  if (kind(sc) == OpKind::Expand) chain.insert(g_.node(sc).src[0]);
+  for (NodeId n : chain) {
+    if (n == xq || n == sx) continue;
+    if (root_set_.count(n) || absorbed_[n]) return false;
+    for (NodeId u : users_[n])
+      if (!chain.count(u)) return false;
+  }
+  for (NodeId n : chain)
+    if (n != sx && n != xq) absorbed_[n] = true;
+  absorbed_[xq] = true;  // produced together with sx
+  actq_pat_[sx] = ActqPattern{x, xq};
+  return true;
+}
+
+void Planner::visit_actq(NodeId sx) {
+  const ActqPattern& p = actq_pat_.at(sx);
+  const NodeId x = p.x;
+  View xv = dev_view_of(x);
+  int xs = vals_[x].slot;
+  if (xv.padded() || !xv.is_contiguous() || xv.offset != 0) {
+    xs = copy_view_to_slot(xv, xs, g_.dtype(x), x);
+    xv = View::contiguous(xv.shape);
+  }
+  ActqStep A;
+  A.x_slot = xs;
+  A.x_dtype = g_.dtype(x);
+  A.n = numel(g_.shape(x));
+  A.xq_slot = new_slot(SlotKind::Temp, DType::F8E4M3, A.n, p.xq);
+  A.sx_slot = new_slot(SlotKind::Temp, DType::F32, 4, sx);
+  A.part_slot = new_slot(SlotKind::Temp, DType::F32, actq_partials_bytes((int64_t)A.n), sx);
+  P_.actqs_.push_back(A);
+  int step = new_step(Step::ACTQ, (int)P_.actqs_.size() - 1, "actq");
+  depend(step, xs);
+  slot_producer_[A.xq_slot] = step;
+  slot_producer_[A.sx_slot] = step;
+  slot_producer_[A.part_slot] = step;
+  Val v;
+  v.k = Val::Dev;
+  v.slot = A.sx_slot;
+  v.view = View::contiguous(g_.shape(sx));
+  vals_[sx] = v;
+  v.slot = A.xq_slot;
+  v.view = View::contiguous(g_.shape(p.xq));
+  vals_[p.xq] = v;
+}
+
 // cast(dot(a, b)) with float dtypes: the GEMM epilogue rounds the f32 accumulator to the dot's
 // dtype and stores it converted to the cast's (graph/ops/core/convert.rs cast of a contraction
 // result, e.g. the matmul-in-f16 policy of graph/pass/amp.rs:16-40 casting back to f32). Taken
@@ -1382,20 +1511,29 @@ bool Planner::match_cast_epilogue(NodeId castn) {
 void Planner::find_patterns() {
   auto order = reachable_multi(g_, P_.roots_);
   consumers_.assign(g_.size(), 0);
+  users_.assign(g_.size(), {});
   for (NodeId id : order)
-    for (NodeId s : g_.node(id).src) consumers_[s]++;
+    for (NodeId s : g_.node(id).src) {
+      consumers_[s]++;
+      users_[s].push_back(id);
+    }
   absorbed_.assign(g_.size(), false);
   for (NodeId id : order) {
     const OpKind k = g_.node(id).op.kind;
     if (k == OpKind::DotGeneral && !absorbed_[id]) match_attention(id);
     if (k == OpKind::Cast && !absorbed_[id]) match_fp8_epilogue(id);
   }
+  for (auto& kv : fp8_pat_) match_actq(kv.second.xq, kv.second.sx);
   for (NodeId id : order)
     if (g_.node(id).op.kind == OpKind::Cast && !absorbed_[id]) match_cast_epilogue(id);
 }
 
 void Planner::visit(NodeId id) {
   const Node& n = g_.node(id);
+  if (actq_pat_.count(id)) {
+    visit_actq(id);
+    return;
+  }
   switch (n.op.kind) {
     case OpKind::Input: {
       auto it = P_.input_slots_.find(id);
@@ -1591,6 +1729,11 @@ void Plan::compile() {
       o << gemm_variant(a) << " b" << G.batch << " m" << G.m << " n" << G.n << " k" << G.k;
       if (G.out_dtype != G.in_dtype && G.alpha_slot < 0) o << " +cast " << dt_name(G.out_dtype);
       s.label = o.str();
+    } else if (s.type == Step::ACTQ) {
+      const ActqStep& A = actqs_[s.index];
+      std::ostringstream o;
+      o << "actq_e4m3 " << dt_name(A.x_dtype) << " n" << A.n;
+      s.label = o.str();
     } else if (s.type == Step::QUANT) {
       const QuantStep& Q = quants_[s.index];
       std::ostringstream o;
@@ -1683,6 +1826,18 @@ void Plan::launch_step(const Step& s) {
     launch_gemm(a, st);
     KU_HIP(hipGetLastError());
     ctx_->profile().launches[(int)Kind::Gemm]++;
+  } else if (s.type == Step::ACTQ) {
+    const ActqStep& A = actqs_[s.index];
+    ActQArgs a;
+    a.x = slot_ptr(slots_, A.x_slot);
+    a.x_type = (int)A.x_dtype;
+    a.n = (int64_t)A.n;
+    a.xq = static_cast<uint8_t*>(slot_ptr(slots_, A.xq_slot));
+    a.sx = static_cast<float*>(slot_ptr(slots_, A.sx_slot));
+    a.partials = static_cast<float*>(slot_ptr(slots_, A.part_slot));
+    launch_actq(a, st);
+    KU_HIP(hipGetLastError());
+    ctx_->profile().launches[(int)Kind::Fused]++;
   } else if (s.type == Step::QUANT) {
     const QuantStep& Q = quants_[s.index];
     QuantArgs a;

@@ -138,8 +138,16 @@ struct AttnStep {
   DType dtype = DType::BF16;
 };
 
+// Per-tensor e4m3 quantisation of a linear layer's activation (the chain the e4m3 pass emits
+// before its GEMM): sx = max|x| * (1/448), xq = e4m3(x * (1/sx)); two kernels, partials scratch.
+struct ActqStep {
+  int x_slot = -1, xq_slot = -1, sx_slot = -1, part_slot = -1;
+  size_t n = 0;
+  DType x_dtype = DType::BF16;
+};
+
 struct Step {
-  enum Type { REGION, GEMM, ATTN, QUANT } type;
+  enum Type { REGION, GEMM, ATTN, QUANT, ACTQ } type;
   int index;             // into regions / gemms / attns
   std::set<int> deps;    // producer step ids
   // compiled launch (regions)
@@ -206,6 +214,7 @@ class Plan {
   std::vector<GemmStep> gemms_;
   std::vector<AttnStep> attns_;
   std::vector<QuantStep> quants_;
+  std::vector<ActqStep> actqs_;
   std::vector<Step> steps_;
   std::vector<int> order_;                 // execution order of steps
   std::map<NodeId, int> input_slots_;
