@@ -269,6 +269,16 @@ size_t ku_hip_codegen(KuGraph *g, const KuNode *roots, size_t n, uint32_t compil
 int32_t ku_hip_linear_e4m3(const KuBackend *b, const void *x, uint32_t x_dtype, const uint8_t *wq, const float *sw,
                            void *y, uint32_t y_dtype, size_t m, size_t n, size_t k, void *stream);
 
+/* ku_hip_linear_e4m3 without any allocation. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under hipGraph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). The scratch (absmax partials, sx, the quantised activation)
+ * is a static device array of 16 MiB + 4352 bytes per GPU, held until the process ends, so
+ * m * k <= 16 MiB (larger sizes return -1 with an error). Runs on the current device and on
+ * `stream` (NULL = the null stream); every call on one GPU shares that GPU's scratch, so calls
+ * that overlap on one GPU race. Returns 0, or -1 with ku_last_error. */
+int32_t ku_hip_linear_e4m3_noalloc(const void *x, uint32_t x_dtype, const uint8_t *wq, const float *sw, void *y,
+                                   uint32_t y_dtype, size_t m, size_t n, size_t k, void *stream);
+
 /* Counters of a backend into out[0..cap): launches per kind (fused, gemm, attention, upload,
  * download), then plans built, constants uploaded and constants cached (plans and constants
  * are cached by graph content, so an equal graph rebuilt per call adds to neither); returns

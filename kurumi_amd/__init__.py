@@ -150,6 +150,7 @@ def _declare(L: C.CDLL) -> None:
         "ku_hip_codegen": ([P, C.POINTER(C.c_uint32), sz, u32, C.c_char_p, sz], sz),
         "ku_hip_profile": ([P, C.POINTER(C.c_uint64), sz], C.c_uint64),
         "ku_hip_linear_e4m3": ([P, P, u32, P, P, P, u32, sz, sz, sz, P], C.c_int32),
+        "ku_hip_linear_e4m3_noalloc": ([P, u32, P, P, P, u32, sz, sz, sz, P], C.c_int32),
         "ku_quant_matmul": ([P, u32, u32, u32, u32, C.c_uint8, sz], u32),
         "ku_quantize": ([C.POINTER(C.c_float), sz, sz, C.c_uint8, sz, u32, C.c_char_p, C.POINTER(C.c_uint16),
                          C.POINTER(C.c_uint16)], None),
@@ -732,6 +733,11 @@ class HipBackend:
         if lib().ku_hip_linear_e4m3(self.h, x, int(x_dtype), wq, sw, y, int(y_dtype), m, n, k, stream) != 0:
             raise KuError(f"ku_hip_linear_e4m3: {last_error()}")
 
+    def linear_e4m3_noalloc(self, x: int, x_dtype: DType, wq: int, sw: int, y: int, y_dtype: DType, m: int,
+                            n: int, k: int, stream: int | None = None) -> None:
+        """ku_hip_linear_e4m3_noalloc (static scratch, no allocation; m * k <= 16 MiB)."""
+        linear_e4m3_noalloc(x, x_dtype, wq, sw, y, y_dtype, m, n, k, stream)
+
     def compile(self, g: Graph, node: int) -> "Plan":
         """kurumi.h:456 ku_plan_compile on this backend (ku_hip_plan_compile_on)."""
         return Plan(g, node, self)
@@ -741,6 +747,13 @@ class HipBackend:
         arr = (C.c_uint64 * len(keys))()
         evals = lib().ku_hip_profile(self.h, arr, len(keys))
         return {"evals": evals, **dict(zip(keys, list(arr)))}
+
+
+def linear_e4m3_noalloc(x: int, x_dtype: DType, wq: int, sw: int, y: int, y_dtype: DType, m: int, n: int, k: int,
+                        stream: int | None = None) -> None:
+    """ku_hip_linear_e4m3_noalloc on device pointers (current device; no backend needed)."""
+    if lib().ku_hip_linear_e4m3_noalloc(x, int(x_dtype), wq, sw, y, int(y_dtype), m, n, k, stream) != 0:
+        raise KuError(f"ku_hip_linear_e4m3_noalloc: {last_error()}")
 
 
 class Plan:

@@ -667,6 +667,28 @@ int32_t ku_hip_linear_e4m3(const KuBackend* b, const void* x, uint32_t x_dtype, 
   });
 }
 
+int32_t ku_hip_linear_e4m3_noalloc(const void* x, uint32_t x_dtype, const uint8_t* wq, const float* sw, void* y,
+                                   uint32_t y_dtype, size_t m, size_t n, size_t k, void* stream) {
+  return guard<int32_t>(-1, [&] {
+    ku::hipbk::LinearE4m3Args a;
+    a.x = x;
+    a.x_type = (int)x_dtype;
+    a.wq = wq;
+    a.sw = sw;
+    a.y = y;
+    a.y_type = (int)y_dtype;
+    a.m = (int64_t)m;
+    a.n = (int64_t)n;
+    a.k = (int64_t)k;
+    try {
+      ku::hipbk::linear_e4m3_noalloc(a, static_cast<hipStream_t>(stream));
+    } catch (const std::runtime_error& e) {
+      throw ku::Error(std::string("ku_hip_linear_e4m3_noalloc: ") + e.what());
+    }
+    return 0;
+  });
+}
+
 uint64_t ku_hip_profile(const KuBackend* b, uint64_t* out, size_t cap) {
   if (!b) return 0;
   auto& pr = b->b->ctx().profile();

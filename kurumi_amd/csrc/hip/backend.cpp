@@ -1,5 +1,7 @@
 #include "backend.h"
 
+#include "kernels/kernels.h"
+
 namespace ku::hipbk {
 
 namespace {
@@ -9,6 +11,8 @@ constexpr size_t kMaxCachedPlans = 8;
 HipBackend::HipBackend(int device) {
   ctx_ = std::make_unique<Context>(device);
   consts_ = std::make_unique<ConstCache>(ctx_.get());
+  ctx_->make_current();
+  init_linear_e4m3_noalloc();  // the no-allocation entry point's scratch on this device
 }
 
 HipBackend::~HipBackend() {

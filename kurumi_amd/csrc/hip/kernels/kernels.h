@@ -99,5 +99,10 @@ struct LinearE4m3Args {
 // bytes of scratch one call needs: absmax partials, sx and the quantised activation (M*K)
 size_t linear_e4m3_scratch_bytes(int64_t m, int64_t k);
 void linear_e4m3(const LinearE4m3Args& a, void* scratch, size_t scratch_bytes, hipStream_t s);
+// The same with scratch in a static device array of kLinearE4m3ScratchBytes per GPU (no
+// allocation): m * k <= kLinearE4m3ScratchBytes - 4352. init_ looks the array up on the current GPU.
+constexpr size_t kLinearE4m3ScratchBytes = (size_t(16) << 20) + 4352;
+void linear_e4m3_noalloc(const LinearE4m3Args& a, hipStream_t s);
+void init_linear_e4m3_noalloc();
 
 }  // namespace ku::hipbk

@@ -13,9 +13,15 @@
 //
 // linear_e4m3 runs the whole layer with scratch the caller (a backend's workspace) provides; the
 // planner runs the same activation kernels as one step before its fp8 GEMM step.
+// linear_e4m3_noalloc runs it with scratch in a file-scope device array instead, for callers that
+// cannot allocate (code under hipGraph capture, serving loops): no hipMalloc, hipFree or other
+// allocating call. Every GPU holds its own copy of the array until the process ends; all calls on
+// one GPU share it (each call's partials and sx are written before they are read, so nothing
+// needs clearing), so calls that overlap on one GPU race.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -253,6 +259,31 @@ void run_linear(const LinearE4m3Args& a, uint8_t* xq, float* partials, float* sx
 constexpr size_t kPartialsOff = 0, kSxOff = 4096, kXqOff = 4096 + 256;
 static_assert(kActqMaxPartials * sizeof(float) <= kSxOff, "partials overflow their scratch part");
 
+// The no-allocation entry point's scratch. In host code `scratch` names a host-side stand-in,
+// never the device memory: its device address on each GPU comes from hipGetSymbolAddress.
+__device__ __align__(256) uint8_t scratch[kLinearE4m3ScratchBytes];
+
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};  // device address of `scratch` on each GPU, set once per GPU
+
+// The current GPU's copy of `scratch` (looked up, with that GPU current, on its first use).
+uint8_t* scratch_on_current_device() {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) throw std::runtime_error(std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) throw std::runtime_error("device index out of range");
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      throw std::runtime_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  return static_cast<uint8_t*>(g_scratch_ptr[dev]);
+}
+
 }  // namespace
 
 size_t linear_e4m3_scratch_bytes(int64_t m, int64_t k) { return kXqOff + (size_t)(m * k); }
@@ -265,5 +296,18 @@ void linear_e4m3(const LinearE4m3Args& a, void* scratch_buf, size_t scratch_byte
   run_linear(a, base + kXqOff, reinterpret_cast<float*>(base + kPartialsOff), reinterpret_cast<float*>(base + kSxOff),
              s);
 }
+
+void linear_e4m3_noalloc(const LinearE4m3Args& a, hipStream_t s) {
+  check_linear(a);
+  if (linear_e4m3_scratch_bytes(a.m, a.k) > kLinearE4m3ScratchBytes)
+    throw std::runtime_error("m * k = " + std::to_string(a.m * a.k) + " exceeds the " +
+                             std::to_string(kLinearE4m3ScratchBytes - kXqOff) +
+                             " bytes the static scratch holds for the quantised activation");
+  uint8_t* base = scratch_on_current_device();
+  run_linear(a, base + kXqOff, reinterpret_cast<float*>(base + kPartialsOff), reinterpret_cast<float*>(base + kSxOff),
+             s);
+}
+
+void init_linear_e4m3_noalloc() { (void)scratch_on_current_device(); }
 
 }  // namespace ku::hipbk
