@@ -78,7 +78,10 @@ KuNode ku_recip(KuGraph *g, KuNode x);
 KuNode ku_sqrt(KuGraph *g, KuNode x);
 KuNode ku_square(KuGraph *g, KuNode x);
 KuNode ku_abs(KuGraph *g, KuNode x);
+KuNode ku_sign(KuGraph *g, KuNode x);  /* kurumi.h:106 */
 KuNode ku_floor(KuGraph *g, KuNode x);
+KuNode ku_ceil(KuGraph *g, KuNode x);  /* kurumi.h:108 */
+KuNode ku_round(KuGraph *g, KuNode x); /* kurumi.h:109 */
 KuNode ku_exp(KuGraph *g, KuNode x);
 KuNode ku_exp2(KuGraph *g, KuNode x);
 KuNode ku_ln(KuGraph *g, KuNode x);
@@ -100,9 +103,12 @@ KuNode ku_sum(KuGraph *g, KuNode x, size_t axis);
 KuNode ku_prod(KuGraph *g, KuNode x, size_t axis);
 KuNode ku_mean(KuGraph *g, KuNode x, size_t axis);
 KuNode ku_reduce_max(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_reduce_min(KuGraph *g, KuNode x, size_t axis);
 KuNode ku_argmax(KuGraph *g, KuNode x, size_t axis);
 KuNode ku_argmin(KuGraph *g, KuNode x, size_t axis);
 KuNode ku_softmax(KuGraph *g, KuNode x, size_t axis);
+KuNode ku_log_softmax(KuGraph *g, KuNode x, size_t axis); /* kurumi.h:201 */
+KuNode ku_logsumexp(KuGraph *g, KuNode x, size_t axis);   /* kurumi.h:202 */
 KuNode ku_squeeze(KuGraph *g, KuNode x, size_t axis);   /* kurumi.h:209 */
 KuNode ku_unsqueeze(KuGraph *g, KuNode x, size_t axis); /* kurumi.h:210 */
 KuNode ku_clamp_min(KuGraph *g, KuNode x, float v);     /* kurumi.h:217 */
@@ -222,6 +228,10 @@ void ku_tensor_bytes(const KuTensor *t, uint8_t *out);
  * (kurumi_core/src/graph/ops/nn/attention.rs:97-133), which kurumi.h does not export. */
 KuNode ku_sdpa_decomposed(KuGraph *g, KuNode q, KuNode k, KuNode v, uint32_t causal);
 KuNode ku_sdpa_fused(KuGraph *g, KuNode q, KuNode k, KuNode v, uint32_t causal);
+
+/* kurumi.h:395: the reference's mixed-precision pass (f16 matmuls): every f32 DotGeneral under
+ * `root` takes f16 casts of its operands and is cast back to f32. Returns the new root. */
+KuNode ku_amp(KuGraph *g, KuNode root);
 
 /* fp8 (OCP e4m3) mixed-precision pass: rewrites linear DotGenerals under `root` into a
  * per-tensor-scaled activation x per-row-scaled weight e4m3 contraction (the e4m3 policy

@@ -15,7 +15,7 @@ from typing import Iterable, Sequence
 
 import numpy as np
 
-__all__ = ["DType", "Graph", "HipBackend", "Plan", "Tensor", "KuError", "lib", "amp_fp8", "KU_ERR"]
+__all__ = ["DType", "Graph", "HipBackend", "Plan", "Tensor", "KuError", "lib", "amp", "amp_fp8", "KU_ERR"]
 
 _PKG = Path(__file__).resolve().parent
 _LIB_PATH = _PKG / "libkurumi_hip.so"
@@ -109,6 +109,7 @@ def _declare(L: C.CDLL) -> None:
         "ku_randn": ([P, psz, sz, C.c_uint64], u32),
         "ku_rand_range": ([P, psz, sz, C.c_uint64, C.c_float, C.c_float], u32),
         "ku_amp_fp8": ([P, u32], u32),
+        "ku_amp": ([P, u32], u32),
         "ku_backend_new": ([u32], P),
         "ku_backend_free": ([P], None),
         "ku_eval": ([P, u32, P], P),
@@ -184,10 +185,10 @@ def _declare(L: C.CDLL) -> None:
         sig[name] = ([P, u32, u32], u32)
     for name in ["ku_neg", "ku_recip", "ku_sqrt", "ku_square", "ku_abs", "ku_floor", "ku_exp", "ku_exp2", "ku_ln",
                  "ku_log2", "ku_sin", "ku_cos", "ku_relu", "ku_detach", "ku_flatten", "ku_t", "ku_sum_all",
-                 "ku_sigmoid", "ku_silu", "ku_tanh", "ku_gelu", "ku_rope"]:
+                 "ku_sigmoid", "ku_silu", "ku_tanh", "ku_gelu", "ku_rope", "ku_sign", "ku_ceil", "ku_round"]:
         sig[name] = ([P, u32], u32)
     for name in ["ku_sum", "ku_prod", "ku_mean", "ku_reduce_max", "ku_argmax", "ku_argmin", "ku_softmax",
-                 "ku_squeeze", "ku_unsqueeze"]:
+                 "ku_squeeze", "ku_unsqueeze", "ku_reduce_min", "ku_logsumexp", "ku_log_softmax"]:
         sig[name] = ([P, u32, sz], u32)
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -455,11 +456,12 @@ for _n, _c in [("neg", "ku_neg"), ("recip", "ku_recip"), ("sqrt", "ku_sqrt"), ("
                ("log2", "ku_log2"), ("sin", "ku_sin"), ("cos", "ku_cos"), ("relu", "ku_relu"),
                ("detach", "ku_detach"), ("flatten", "ku_flatten"), ("t", "ku_t"), ("sum_all", "ku_sum_all"),
                ("sigmoid", "ku_sigmoid"), ("silu", "ku_silu"), ("tanh", "ku_tanh"), ("gelu", "ku_gelu"),
-               ("rope", "ku_rope")]:
+               ("rope", "ku_rope"), ("sign", "ku_sign"), ("ceil", "ku_ceil"), ("round", "ku_round")]:
     _add_simple(_n, _c, 1)
 for _n, _c in [("sum", "ku_sum"), ("prod", "ku_prod"), ("mean", "ku_mean"), ("reduce_max", "ku_reduce_max"),
                ("argmax", "ku_argmax"), ("argmin", "ku_argmin"), ("softmax", "ku_softmax"),
-               ("squeeze", "ku_squeeze"), ("unsqueeze", "ku_unsqueeze")]:
+               ("squeeze", "ku_squeeze"), ("unsqueeze", "ku_unsqueeze"), ("reduce_min", "ku_reduce_min"),
+               ("logsumexp", "ku_logsumexp"), ("log_softmax", "ku_log_softmax")]:
     _add_simple(_n, _c, 3)
 
 
@@ -607,6 +609,11 @@ def quantize(w: np.ndarray, bits: int, group_size: int, symmetric: bool):
                       packed.ctypes.data_as(C.c_char_p), scales.ctypes.data_as(C.POINTER(C.c_uint16)),
                       None if mins is None else mins.ctypes.data_as(C.POINTER(C.c_uint16)))
     return packed, scales, mins
+
+
+def amp(g: Graph, root: int) -> int:
+    """The reference's mixed-precision pass (graph/pass/amp.rs:16-40; kurumi.h:395 ku_amp)."""
+    return g._n("ku_amp", root)
 
 
 def amp_fp8(g: Graph, root: int) -> int:

@@ -148,6 +148,9 @@ KU_UN(ku_sqrt, gr.sqrt(x))
 KU_UN(ku_square, gr.square(x))
 KU_UN(ku_abs, gr.max(x, gr.neg(x)))
 KU_UN(ku_floor, gr.floor(x))
+KU_UN(ku_ceil, gr.ceil(x))
+KU_UN(ku_round, gr.round(x))
+KU_UN(ku_sign, gr.sign(x))
 KU_UN(ku_exp, gr.exp(x))
 KU_UN(ku_exp2, gr.exp2(x))
 KU_UN(ku_ln, gr.ln(x))
@@ -172,6 +175,9 @@ KU_AX(ku_sum, gr.sum(x, axis))
 KU_AX(ku_prod, gr.prod(x, axis))
 KU_AX(ku_mean, gr.mean(x, axis))
 KU_AX(ku_reduce_max, gr.reduce_max(x, axis))
+KU_AX(ku_reduce_min, gr.reduce_min(x, axis))
+KU_AX(ku_logsumexp, gr.logsumexp(x, axis))
+KU_AX(ku_log_softmax, gr.log_softmax(x, axis))
 KU_AX(ku_argmax, gr.argreduce(x, axis, ku::ArgKind::Max))
 KU_AX(ku_argmin, gr.argreduce(x, axis, ku::ArgKind::Min))
 KU_AX(ku_softmax, gr.softmax(x, axis))
@@ -299,6 +305,9 @@ KuNode ku_randn(KuGraph* g, const size_t* shape, size_t rank, uint64_t seed) {
 }
 KuNode ku_rand_range(KuGraph* g, const size_t* shape, size_t rank, uint64_t seed, float lo, float hi) {
   return build(g, "ku_rand_range", [&](ku::Graph& gr) { return gr.rand_range(mk_shape(shape, rank), seed, lo, hi); });
+}
+KuNode ku_amp(KuGraph* g, KuNode root) {
+  return build(g, "ku_amp", [&](ku::Graph& gr) { return ku::amp(gr, root); });
 }
 KuNode ku_amp_fp8(KuGraph* g, KuNode root) {
   return build(g, "ku_amp_fp8", [&](ku::Graph& gr) { return ku::amp_fp8(gr, root); });

@@ -372,6 +372,29 @@ NodeId Graph::ln(NodeId a) {
   return mul(l, c);
 }
 NodeId Graph::relu(NodeId a) { NodeId z = scalar(a, 0.f); return max(a, z); }
+// elementwise.rs:126-135: select(0 < x, 1, 0) + select(x < 0, -1, 0)
+NodeId Graph::sign(NodeId a) {
+  NodeId z = scalar(a, 0.f);
+  NodeId pos = cmp_lt(z, a);
+  NodeId ng = cmp_lt(a, z);
+  NodeId one = scalar(a, 1.f);
+  NodeId neg1 = scalar(a, -1.f);
+  NodeId p = where(pos, one, z);
+  NodeId n = where(ng, neg1, z);
+  return add(p, n);
+}
+// elementwise.rs:164-168: ceil(x) = -floor(-x)
+NodeId Graph::ceil(NodeId a) {
+  NodeId nx = neg(a);
+  NodeId f = floor(nx);
+  return neg(f);
+}
+// elementwise.rs:171-175: round(x) = floor(x + 0.5)
+NodeId Graph::round(NodeId a) {
+  NodeId h = scalar(a, 0.5f);
+  NodeId s = add(a, h);
+  return floor(s);
+}
 NodeId Graph::square(NodeId a) { return mul(a, a); }
 // trig.rs:16-20: cos(x) = sin(x + pi/2)
 NodeId Graph::cos(NodeId a) {
@@ -542,6 +565,33 @@ NodeId Graph::broadcast_back(NodeId reduced, const Shape& full, size_t axis) {
   keep.insert(keep.begin() + axis, 1);
   NodeId r = reshape(reduced, keep);
   return expand(r, full);
+}
+// reduce.rs:54-58: min over an axis is -reduce_max(-x)
+NodeId Graph::reduce_min(NodeId a, size_t axis) {
+  check_id("reduce_min", a);
+  NodeId nx = neg(a);
+  NodeId m = reduce_max(nx, axis);
+  return neg(m);
+}
+// reduce.rs:115-124: m + ln(sum(exp(x - m))) with m = reduce_max(x)
+NodeId Graph::logsumexp(NodeId a, size_t axis) {
+  check_id("logsumexp", a);
+  const Shape full = shape(a);
+  NodeId m = reduce_max(a, axis);
+  NodeId mb = broadcast_back(m, full, axis);
+  NodeId sh = sub(a, mb);
+  NodeId e = exp(sh);
+  NodeId s = sum(e, axis);
+  NodeId l = ln(s);
+  return add(l, m);
+}
+// activation.rs:132-137: x - logsumexp(x) broadcast back
+NodeId Graph::log_softmax(NodeId a, size_t axis) {
+  check_id("log_softmax", a);
+  const Shape full = shape(a);
+  NodeId lse = logsumexp(a, axis);
+  NodeId lb = broadcast_back(lse, full, axis);
+  return sub(a, lb);
 }
 NodeId Graph::mean(NodeId a, size_t axis) {
   check_id("mean", a);

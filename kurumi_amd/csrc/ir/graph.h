@@ -130,6 +130,9 @@ class Graph {
   NodeId exp(NodeId a);             // explog.rs:9-13
   NodeId ln(NodeId a);              // explog.rs:16-20
   NodeId relu(NodeId a);            // activation.rs:17-20
+  NodeId sign(NodeId a);            // elementwise.rs:126-135
+  NodeId ceil(NodeId a);            // elementwise.rs:164-168
+  NodeId round(NodeId a);           // elementwise.rs:171-175 (floor(x + 0.5))
   NodeId square(NodeId a);
   NodeId cos(NodeId a);             // trig.rs: sin(x + pi/2)
   NodeId tanh(NodeId a);            // trig.rs:50-58: 2*sigmoid(2x) - 1
@@ -140,6 +143,9 @@ class Graph {
   NodeId randn(const Shape& shape, uint64_t seed);                    // random.rs:28-40
   NodeId rand_range(const Shape& shape, uint64_t seed, float lo, float hi);  // random.rs:43-49
   NodeId mean(NodeId a, size_t axis);
+  NodeId reduce_min(NodeId a, size_t axis);   // reduce.rs:54-58
+  NodeId logsumexp(NodeId a, size_t axis);    // reduce.rs:115-124
+  NodeId log_softmax(NodeId a, size_t axis);  // activation.rs:132-137
 
   // reductions (reduce.rs:8-43)
   NodeId sum(NodeId a, size_t axis);
@@ -198,6 +204,10 @@ class Graph {
 // inspection (graph/inspect.rs:10-55)
 std::vector<NodeId> reachable_multi(const Graph& g, const std::vector<NodeId>& roots);
 std::string dump(const Graph& g, NodeId root);
+
+// The reference's mixed-precision pass (graph/pass/amp.rs:16-40): f32 DotGenerals run in f16
+// (operands cast down, result cast back up). Returns the new root.
+NodeId amp(Graph& g, NodeId root);
 
 // The build's fp8 mixed-precision pass: rewrites an f32/bf16 `DotGeneral` whose rhs is a
 // constant weight into an e4m3 contraction with a per-row weight scale and a per-tensor
