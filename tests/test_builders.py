@@ -97,7 +97,8 @@ def test_builders_on_device_match_oracle(hip, dt):
 
 @pytest.mark.gpu
 def test_amp_graph_on_device_matches_oracle(hip):
-    """The amped linear: the f16 contraction and its cast back become one f16 GEMM + cast epilogue."""
+    """The amped linear runs on the f16 MFMA GEMM; its cast back to f32 joins the relu's region
+    (a widening cast that feeds more elementwise work reads the 2-byte GEMM output)."""
     g = Graph()
     x = g.input([96, 256], DType.F32)
     w = g.constant(randn([256, 320], 7, 0.05))
@@ -105,7 +106,7 @@ def test_amp_graph_on_device_matches_oracle(hip):
     amped = K.amp(g, y)
     feeds = {x: Tensor.from_numpy(randn([96, 256], 8))}
     plan = hip.plan(g, [amped], feeds)
-    assert any(s.startswith("gemm_mfma_f16") and "+cast F32" in s for s in plan.steps()), plan.steps()
+    assert any(s.startswith("gemm_mfma_f16") for s in plan.steps()), plan.steps()
     got = hip.eval_with(g, amped, feeds).numpy()
     want = interpret(g, [amped], feeds)[0].numpy()
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="amp on device vs oracle")
