@@ -297,7 +297,17 @@ struct Gen {
   void emit_line_node(int ni);
   void emit_red_init(int ni);
   void emit_red_update(int ni, const std::string& k_expr, const std::string& j);
+  void emit_red_chunk_arg(int ni);
   void emit_red_finish(int ni, int phase);
+  // A float ArgReduce over vector chunks folds per chunk: the chunk's extreme (one maxNum/minNum
+  // tree), one strict comparison with the running best, and a conditional copy of the chunk's
+  // values; the index inside the winning chunk is found once per thread at the end. Per element
+  // that is about a third of the compare-and-select-index work of a per-element fold.
+  bool chunk_arg(int ni) const {
+    const RNode& n = node(ni);
+    return n.kind == (int)OpKind::ArgReduce && V >= 2 && fvalued(node(n.in[0]).dtype) && !flat;
+  }
+  bool chunk_arg_packed(int ni) const { return chunk_arg(ni) && node(node(ni).in[0]).dtype == DType::BF16 && V % 2 == 0; }
   std::string leaf_base(int leaf) const;
   std::string generate(RegionCode* rc);
   std::string finish(const std::string& prefix, RegionCode* rc) {
@@ -816,6 +826,12 @@ void Gen::emit_red_init(int ni) {
     else init = mx ? int_min(in) : int_max(in);
     o << "  " << ctype(in) << " bv" << r << " = " << init << "; " << aix() << " bi" << r << " = " << aix_none()
       << "; bool bn" << r << " = false;\n";
+    if (chunk_arg(ni)) {
+      // the winning chunk: its first element index and its values (bf16 values two to a word)
+      o << "  " << aix() << " bc" << r << " = " << aix_none() << "; ";
+      if (chunk_arg_packed(ni)) o << "u32 sw" << r << "[" << V / 2 << "] = {};\n";
+      else o << "float sv" << r << "[" << V << "] = {};\n";
+    }
     return;
   }
   DType acc = n.dtype;
@@ -862,6 +878,30 @@ void Gen::emit_red_update(int ni, const std::string& k_expr, const std::string& 
   }
 }
 
+// One chunk of a float ArgReduce (see chunk_arg): the chunk's extreme by maxNum / minNum (NaN
+// never wins, as in the per-element rule), a strict comparison with the running best so the first
+// chunk holding the best value keeps it, and the reference's NaN-at-index-0 flag from element 0.
+void Gen::emit_red_chunk_arg(int ni) {
+  const RNode& n = node(ni);
+  std::string r = std::to_string(ni);
+  const bool mx = n.arg == ArgKind::Max;
+  const std::string f = mx ? "fmaxf" : "fminf", cmp = mx ? ">" : "<";
+  o << "      { float cm_ = " << val(n.in[0], "0") << ";\n";
+  o << "        #pragma unroll\n        for (int j = 1; j < " << V << "; ++j) cm_ = " << f << "(cm_, " << val(n.in[0], "j")
+    << ");\n";
+  o << "        if (ch == 0u && " << val(n.in[0], "0") << " != " << val(n.in[0], "0") << ") bn" << r << " = true;\n";
+  o << "        const bool up_ = cm_ " << cmp << " bv" << r << ";\n";
+  o << "        bv" << r << " = up_ ? cm_ : bv" << r << "; bc" << r << " = up_ ? (" << aix() << ")(ch * " << V << "u) : bc" << r
+    << ";\n";
+  if (chunk_arg_packed(ni))
+    o << "        #pragma unroll\n        for (int jj = 0; jj < " << V / 2 << "; ++jj) sw" << r << "[jj] = up_ ? pack_bf16_exact("
+      << val(n.in[0], "2 * jj") << ", " << val(n.in[0], "2 * jj + 1") << ") : sw" << r << "[jj];\n";
+  else
+    o << "        #pragma unroll\n        for (int j = 0; j < " << V << "; ++j) sv" << r << "[j] = up_ ? " << val(n.in[0], "j")
+      << " : sv" << r << "[j];\n";
+  o << "      }\n";
+}
+
 // cross-lane fold of a reduction (butterfly within the wave, LDS across waves)
 void Gen::emit_red_finish(int ni, int phase) {
   const RNode& n = node(ni);
@@ -881,6 +921,16 @@ void Gen::emit_red_finish(int ni, int phase) {
     if (fvalued(n.dtype) || in == DType::F32) return "acc" + r + " = fmaxf(acc" + r + ", " + ov + ");";
     return "acc" + r + " = (" + ov + " > acc" + r + ") ? " + ov + " : acc" + r + ";";
   };
+  if (chunk_arg(ni)) {
+    // the index of the first element of the winning chunk equal to the best value
+    o << "  if (bc" << r << " != " << aix_none() << ") {\n    " << aix() << " bj_ = " << V - 1 << ";\n";
+    if (chunk_arg_packed(ni))
+      o << "    #pragma unroll\n    for (int j = " << V - 1 << "; j >= 0; --j) { const float v_ = __uint_as_float((j & 1) ? (sw" << r
+        << "[j >> 1] & 0xffff0000u) : (sw" << r << "[j >> 1] << 16)); if (v_ == bv" << r << ") bj_ = j; }\n";
+    else
+      o << "    #pragma unroll\n    for (int j = " << V - 1 << "; j >= 0; --j) if (sv" << r << "[j] == bv" << r << ") bj_ = j;\n";
+    o << "    bi" << r << " = bc" << r << " + bj_;\n  }\n";
+  }
   int wl = std::min(TPL, 64);
   const bool fsum = n.kind == (int)OpKind::Sum && (fvalued(n.dtype) || in == DType::F32);
   const bool fmax = n.kind == (int)OpKind::ReduceMax && (fvalued(n.dtype) || in == DType::F32);
@@ -1064,6 +1114,10 @@ std::string Gen::generate(RegionCode* rc) {
     for (size_t i = 0; i < R.nodes.size(); ++i)
       if (need[p].count((int)i)) emit_full_node((int)i, p, cexpr);
     for (int r : reds) {
+      if (chunk_arg(r)) {
+        emit_red_chunk_arg(r);
+        continue;
+      }
       o << "      #pragma unroll\n      for (int j = 0; j < " << V << "; ++j) {\n";
       emit_red_update(r, "ch * " + std::to_string(V) + "u + j", "j");
       o << "      }\n";

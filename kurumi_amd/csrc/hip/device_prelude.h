@@ -36,14 +36,17 @@ KD float bf16_ld(u16 h) { return __uint_as_float(((u32)h) << 16); }
 // (the same result as the bit formula u + 0x7fff + lsb >> 16, NaN -> (u >> 16) | 0x40, for all
 // 2^32 f32 inputs on gfx950)
 KD u16 bf16_st(float f) { return __builtin_bit_cast(u16, (__bf16)f); }
-KD float rbf16(float f) { return bf16_ld(bf16_st(f)); }
-// two roundings with one v_cvt_pk_bf16_f32
 typedef __bf16 ku_bf16x2 __attribute__((ext_vector_type(2)));
 typedef float ku_f32x2 __attribute__((ext_vector_type(2)));
+// f rounded to bf16, as an f32: v_cvt_pk_bf16_f32 with 0 as the low operand leaves bf16(f) in the
+// high half over a zero low half, which is that value's f32 pattern (one instruction, no unpack)
+KD float rbf16(float f) {
+  return __uint_as_float(__builtin_bit_cast(u32, __builtin_convertvector((ku_f32x2){0.f, f}, ku_bf16x2)));
+}
+// two roundings: one instruction each (a shared v_cvt_pk_bf16_f32 would need two unpacks)
 KD void rbf16x2(float& a, float& b) {
-  const u32 p = __builtin_bit_cast(u32, __builtin_convertvector((ku_f32x2){a, b}, ku_bf16x2));
-  a = __uint_as_float(p << 16);
-  b = __uint_as_float(p & 0xffff0000u);
+  a = rbf16(a);
+  b = rbf16(b);
 }
 // bf16-exact floats (low 16 bits zero) -> two packed bf16 patterns
 KD u32 pack_bf16_exact(float lo, float hi) { return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u); }
