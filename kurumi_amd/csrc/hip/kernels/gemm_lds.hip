@@ -119,9 +119,9 @@ __device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KU_LDS void*)l, 16, voff, soff, 0, 0);
 }
 
-template <int E, bool BNMAJ, int OT, int BM, int BN, int WM, int WN, bool BUF>
+template <int E, bool BNMAJ, int OT, int BM, int BN, int WM, int WN, bool BUF, int OCC>
 __global__ void __launch_bounds__(WM* WN * 64)
-    __attribute__((amdgpu_waves_per_eu((WM * WN + 3) / 4, (WM * WN + 3) / 4))) gemm_lds_k(GemmArgs a) {
+    __attribute__((amdgpu_waves_per_eu(OCC, OCC))) gemm_lds_k(GemmArgs a) {
   constexpr int NW = WM * WN, NT = NW * 64;
   constexpr int EB = (E == E_FP8) ? 1 : 2;
   constexpr int KE = KB / EB;  // K elements per stage
@@ -400,14 +400,14 @@ bool spans_fit(const GemmArgs& a) {
   return aspan + 16 <= lim && bspan + 16 <= lim;
 }
 
-template <int E, bool BNMAJ, int OT, int BM, int BN, int WM, int WN>
+template <int E, bool BNMAJ, int OT, int BM, int BN, int WM, int WN, int OCC = (WM * WN + 3) / 4>
 void launch_tile(const GemmArgs& a, hipStream_t s) {
   const int tm = (int)((a.m + BM - 1) / BM), tn = (int)((a.n + BN - 1) / BN);
   dim3 grid((unsigned)(tm * tn), (unsigned)a.batch);
   if (spans_fit(a))
-    hipLaunchKernelGGL((gemm_lds_k<E, BNMAJ, OT, BM, BN, WM, WN, true>), grid, dim3(WM * WN * 64), 0, s, a);
+    hipLaunchKernelGGL((gemm_lds_k<E, BNMAJ, OT, BM, BN, WM, WN, true, OCC>), grid, dim3(WM * WN * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((gemm_lds_k<E, BNMAJ, OT, BM, BN, WM, WN, false>), grid, dim3(WM * WN * 64), 0, s, a);
+    hipLaunchKernelGGL((gemm_lds_k<E, BNMAJ, OT, BM, BN, WM, WN, false, OCC>), grid, dim3(WM * WN * 64), 0, s, a);
 }
 
 int cu_count() {
@@ -433,9 +433,19 @@ bool rows192(const GemmArgs& a) {
   return (double)r192 * 192 * 1.1 < (double)r256 * 256;
 }
 
+// small K (one or two stages): 128 x 128 tiles of 4 waves, two work-groups per CU, so one
+// group's epilogue stores run under the other's loads and MFMAs
+// (measured on the batched [8, 2048, 128] x [8, 128, 2048] bf16 GEMM: 31.3 -> 27.5 us against
+// 256 x 256 tiles; issuing both stages up front, or storing C non-temporally, changed nothing)
+bool small_k(const GemmArgs& a) {
+  const int64_t kbytes = a.k * (a.in_type == GT_F8E4M3 ? 1 : 2);
+  return kbytes <= 2 * 128;
+}
+
 template <int E, bool BNMAJ, int OT>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
-  if (rows192(a)) launch_tile<E, BNMAJ, OT, 192, 256, 2, 4>(a, s);
+  if (small_k(a)) launch_tile<E, BNMAJ, OT, 128, 128, 2, 2, 2>(a, s);
+  else if (rows192(a)) launch_tile<E, BNMAJ, OT, 192, 256, 2, 4>(a, s);
   else launch_tile<E, BNMAJ, OT, 256, 256, 2, 4>(a, s);
 }
 
@@ -475,7 +485,7 @@ bool gemm_lds_ok(const GemmArgs& a) {
 std::string gemm_lds_name(const GemmArgs& a) {
   std::string n = a.in_type == GT_F8E4M3 ? "gemm_mfma_e4m3" : a.in_type == GT_F16 ? "gemm_mfma_f16" : "gemm_mfma_bf16";
   n += a.sbk == 1 ? "_nt" : "_nn";
-  n += rows192(a) ? "_192x256" : "_256x256";
+  n += small_k(a) ? "_128x128" : rows192(a) ? "_192x256" : "_256x256";
   if (!spans_fit(a)) n += "_a64";
   return n;
 }
