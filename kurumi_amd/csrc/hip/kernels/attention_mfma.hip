@@ -16,11 +16,14 @@
 // holds key 8*(i/4) + 4*h + i%4, i.e. key k sits at slot swap(bit2, bit3)(k). V^T is written to
 // LDS in that slot order, so both operands read 16 contiguous bytes per lane.
 //
-// Work-group: NW waves of 32*QT queries each, blocks of BK = 64 keys staged global -> registers
-// -> LDS (K row-major, V transposed), double-buffered with one barrier per block. Causal q-tiles are
-// issued heaviest first, and every head's tiles land on one XCD so its K/V stay in that L2.
+// Work-group: NW waves of 32 queries each (a q-tile of 32*NW queries), blocks of BK = 64 keys
+// staged global -> LDS by DMA, double-buffered with one barrier per block. The grid is persistent
+// (two work-groups per CU), each work-group walking a fixed sequence of q-tiles with the pipeline
+// running across tile boundaries; causal q-tiles are taken heaviest first, and every head's tiles
+// land on one XCD so its K/V stay in that L2.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <stdexcept>
@@ -94,16 +97,32 @@ __device__ __forceinline__ u32x4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 constexpr float RESCALE = 8.f;
 
 
-// QT 32-query tiles per wave: QT = 2 halves the LDS bytes per MFMA (every K / V fragment feeds
-// two MFMAs) at the price of one wave per SIMD.
+// One q-tile of one head, as the persistent loop below walks them. A tile past the last one has
+// no key blocks and its queries start at the sequence end, so every load of it reads zeros.
+// 32-bit fields: the scalar registers are the kernel's scarce resource (S < 2^24 here).
+struct Tile {
+  int head;  // q / k / v / o head
+  int q0;    // first query
+  int nkv;   // key blocks holding keys the tile needs
+  int nkb;   // blocks the loop runs: nkv rounded up to even (the extra block is fully masked)
+};
+
+// Persistent work-groups (about two per CU): work-group b runs its tiles one after another (see
+// tile_at), and the software pipeline runs straight across tile boundaries, so a tile's prologue
+// (Q fragments, the first K / V blocks, the first S^T) and epilogue overlap the neighbouring
+// tile's blocks instead of leaving the CU to the other work-group.
 //
 // Software pipeline per block kb (one barrier each): the S^T MFMAs of block kb+1 are independent
-// of the softmax instructions of block kb, so the two interleave; then the P.V MFMAs of block kb run while the
-// staged K of block kb+2 and V of block kb+1 are written to LDS. K and V have separate
-// double buffers, K one block ahead of V.
-template <int D, int DT, int NW, int QT>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 2 : 1, QT == 1 ? 2 : 1)))
+// of the softmax instructions of block kb, so the two interleave; then the P.V MFMAs of block kb
+// run while K of block kb+2 and V of block kb+1 land in LDS. K and V have separate double
+// buffers, K one block ahead of V. Past a tile's last block those are the next tile's blocks 0
+// and 1: its Q fragments are loaded once the current tile's last S^T has been issued, and the
+// last block's "next S^T" is the next tile's first, so every tile but a work-group's first
+// starts with its K0, K1, V0 and first scores in place.
+template <int D, int DT, int NW>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn_mfma_k(AttnArgs a) {
+  constexpr int QT = 1;                  // 32-query tiles per wave
   constexpr int QW = 32 * QT, BQ = QW * NW;
   constexpr int RB = D * 2;              // bytes per K / V row in LDS (no padding: swizzled)
   constexpr int W = 256 / RB;            // rows per 256-byte bank window (64 banks)
@@ -116,38 +135,56 @@ attn_mfma_k(AttnArgs a) {
   // every block a wave needs starts at or before the wave's first query, so a lane is never
   // fully masked in a block it needs
   static_assert(BK % 32 == 0 && (QW % BK == 0 || BK % QW == 0), "block / wave alignment");
-  // K buffers 0, 1 then V buffers 0, 1
-  __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[4 * TBYTES];
+  // K buffers 0, 1 then V buffers 0, 1; the last one doubles as the epilogue's staging area
+  // (4 KB per wave), so it is at least that large
+  constexpr int STAGE = NW * 4096;
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[3 * TBYTES + (TBYTES > STAGE ? TBYTES : STAGE)];
   KU_LDS unsigned char* lds = (KU_LDS unsigned char*)lds_raw;
 
   // the wave index is uniform: kept in an SGPR, so the DMA destinations (M0) need no VALU work
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5,
             qc = lane & 31;
-  const int64_t S = a.s;
-  const int nqt = (int)((S + BQ - 1) / BQ);
-  // heaviest causal tiles first; tile ids with equal head stay on one XCD (bh % 8 == 0 case)
-  const int id = blockIdx.x;
-  const int head = id % (int)a.bh;
-  const int qt = a.causal ? nqt - 1 - id / (int)a.bh : id / (int)a.bh;
-  const int64_t q0 = (int64_t)qt * BQ;
-  const int64_t qw = q0 + wave * QW;  // first query of this wave
-  const int64_t base = (int64_t)head * S * D;
-  // raw buffer loads: rows past the sequence read as zero, no branches
+  const int S = (int)a.s;
+  const int64_t HS = (int64_t)S * D;  // elements per head
+  const int bh = (int)a.bh;
+  const int nqt = (S + BQ - 1) / BQ;
+  const int64_t ntiles = (int64_t)nqt * bh;
+  const int64_t G = gridDim.x;
   const uint32_t hb = (uint32_t)(S * D * 2);  // bytes per head
-  const auto Q = rsrc(static_cast<const uint16_t*>(a.q) + base, hb);
+  // Tile t is head t % bh, q-tile t / bh (causal: heaviest first). Work-group b takes tile
+  // r*G + b in round r, and in odd rounds the tile at the mirrored position among the
+  // work-groups of its XCD (b % 8 kept): the causal tiles' sizes even out over a work-group's
+  // rounds, and with bh % 8 == 0 every tile of a head runs on one XCD, whose L2 keeps its K / V.
+  auto tile_at = [&](int r) {
+    const int64_t b = blockIdx.x;
+    const bool mirror = (r & 1) && (G & 7) == 0;
+    const int64_t t = (int64_t)r * G + (mirror ? (b & 7) + 8 * (G / 8 - 1 - (b >> 3)) : b);
+    Tile T{0, S, 0, 0};
+    if (t < ntiles) {
+      const int ti = (int)t, qt = a.causal ? nqt - 1 - ti / bh : ti / bh;
+      T.head = ti % bh;
+      T.q0 = qt * BQ;
+      const int kend = a.causal ? (T.q0 + BQ < S ? T.q0 + BQ : S) : S;  // keys the tile needs
+      T.nkv = (kend + BK - 1) / BK;
+      T.nkb = (T.nkv + 1) & ~1;
+    }
+    return T;
+  };
 
+  // raw buffer loads: rows past the sequence read as zero, no branches
   // Q fragments (B operand of S^T): lane holds query qw + 32u + qc, dims 16*s + 8*h .. +7
   u32x4 qf[QT][DS];
+  auto load_q = [&](const Tile& T) {
+    const auto Q = rsrc(static_cast<const uint16_t*>(a.q) + T.head * HS, hb);
+    const int qw = T.q0 + wave * QW;
 #pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const int64_t qi = qw + 32 * u + qc;
-    const uint32_t off = qi < S ? (uint32_t)(qi * D * 2) + h * 16 : hb;
+    for (int u = 0; u < QT; ++u) {
+      const int qi = qw + 32 * u + qc;
+      const uint32_t off = qi < S ? (uint32_t)(qi * D * 2) + h * 16 : hb;
 #pragma unroll
-    for (int s = 0; s < DS; ++s) qf[u][s] = bload(Q, off + s * 32);
-  }
-
-  const int64_t kend = a.causal ? (q0 + BQ < S ? q0 + BQ : S) : S;  // keys this tile needs
-  const int nkb = (int)((kend + BK - 1) / BK);
+      for (int s = 0; s < DS; ++s) qf[u][s] = bload(Q, off + s * 32);
+    }
+  };
 
   // K and V blocks go global -> LDS by DMA (buffer_load ... lds: lane l of a wave writes bytes
   // 16l..16l+15 of the wave's 1 KB destination; offsets past the head read as zeros). The LDS
@@ -160,17 +197,21 @@ attn_mfma_k(AttnArgs a) {
   auto kswz = [](int r) { return (r / W) % (16 / W); };
   auto vswz = [](int r) { return 4 * ((r / W) % (4 / W)); };
   // The block offset moves the descriptor's base (scalar work; the byte count shrinks with it, so
-  // blocks past the head still read zeros) and the per-lane offsets stay loop-invariant.
-  const uint16_t* kp = static_cast<const uint16_t*>(a.k) + base;
-  const uint16_t* vp = static_cast<const uint16_t*>(a.v) + base;
-  auto dma = [&](const uint16_t* src, int kb, KU_LDS unsigned char* dst, bool isv) {
-    const uint32_t k0b = kb < nkb ? (uint32_t)kb * BK * RB : hb;
-    const auto R = rsrc(reinterpret_cast<const unsigned char*>(src) + k0b, hb - k0b);
+  // blocks past the tile's keys read zeros) and the per-lane offsets stay loop-invariant.
+  const uint16_t* kp = static_cast<const uint16_t*>(a.k);
+  const uint16_t* vp = static_cast<const uint16_t*>(a.v);
+  auto dma = [&](const uint16_t* src, int head, int nkv, int kb, KU_LDS unsigned char* dst, bool isv) {
+    const uint32_t k0b = kb < nkv ? (uint32_t)kb * BK * RB : hb;
+    const auto R = rsrc(reinterpret_cast<const unsigned char*>(src + head * HS) + k0b, hb - k0b);
+    // the wave's first destination, recomputed at every call (opaque to the optimiser): hoisted,
+    // the M0 values of all DMAs would stay live in SGPRs across the loop and spill
+    KU_LDS unsigned char* wd = dst + wave * 1024;
+    asm volatile("" : "+s"(wd));
 #pragma unroll
     for (int i = 0; i < NBLK; ++i) {
       const int blk = i * NW + wave, r = blk * (1024 / RB) + lane / CPR, pc = lane % CPR;
       const int cc = pc ^ (isv ? vswz(r) : kswz(r));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(R, (KU_LDS void*)(dst + blk * 1024), 16, r * RB + cc * 16, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(R, (KU_LDS void*)(wd + i * NW * 1024), 16, r * RB + cc * 16, 0, 0, 0);
     }
   };
   auto kbuf = [&](int i) { return lds + i * TBYTES; };
@@ -196,166 +237,191 @@ attn_mfma_k(AttnArgs a) {
 
   f32x16 o[QT][DTL];
   float mc[QT], l[QT];
-#pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    mc[u] = -INFINITY;
-    l[u] = 0.f;
-#pragma unroll
-    for (int t = 0; t < DTL; ++t)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) o[u][t][v] = 0.f;
-  }
   const float c = a.scale * LOG2E;
-  const bool live = qw < S;  // wave-uniform: waves past the sequence only help staging
+  int round = 0;
+  Tile C = tile_at(0), N = tile_at(1);  // this work-group's current and next tile
+  int qw = C.q0 + wave * QW;            // first query of this wave in the current tile
 
-  dma(kp, 0, kbuf(0), false);
-  dma(vp, 0, vbuf(0), true);
-  dma(kp, 1, kbuf(1), false);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
   // One block: softmax of sc (this block's S^T) and S^T of the next block into sn. The loop runs
   // two blocks per trip with the two score sets swapping roles, so no registers are copied.
   // The parity of kb is a compile-time constant, so every LDS address is a loop-invariant
-  // per-lane value plus an immediate.
+  // per-lane value plus an immediate. Waves whose queries lie past the sequence run the same
+  // instructions on zero queries (their results are never stored), so every wave computes the
+  // next tile's first scores.
   auto block = [&](int kb, f32x16 (&sc)[QT][2], f32x16 (&sn)[QT][2], auto par) __attribute__((always_inline)) {
     constexpr int P = decltype(par)::value;
-    // K of block kb+2 and V of block kb+1 into the buffers the previous block freed
-    dma(kp, kb + 2, kbuf(P), false);
-    dma(vp, kb + 1, vbuf(P ^ 1), true);
-    const int64_t k0 = (int64_t)kb * BK;
+    // K of block kb+2 and V of block kb+1 into the buffers the previous block freed: this tile's
+    // while it has them, then the next tile's first ones
+    const bool kc = kb + 2 < C.nkb, vc = kb + 1 < C.nkb;
+    dma(kp, kc ? C.head : N.head, kc ? C.nkv : N.nkv, kc ? kb + 2 : kb + 2 - C.nkb, kbuf(P), false);
+    dma(vp, vc ? C.head : N.head, vc ? C.nkv : N.nkv, vc ? kb + 1 : kb + 1 - C.nkb, vbuf(P ^ 1), true);
+    const int k0 = kb * BK;
     u32x4 pf[QT][4];
-    if (live) {
 #pragma unroll
-      for (int u = 0; u < QT; ++u) {
-        // mask keys past the sequence and (causal) keys after the query: key k0 + off(t, v) + 4h
-        // is dropped when off(t, v) > lim, off(t, v) = 32t + 8(v/4) + v%4 a constant per register
-        if ((k0 + BK > S) || (a.causal && k0 + BK - 1 > qw + 32 * u)) {
-          const int64_t qi = qw + 32 * u + qc;
-          const int64_t last = a.causal && qi < S - 1 ? qi : S - 1;  // last visible key
-          const int lim = (int)(last - k0) - 4 * h;
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int v = 0; v < 16; ++v)
-              if (t * 32 + (v >> 2) * 8 + (v & 3) > lim) sc[u][t][v] = -INFINITY;
-        }
-        float bm = sc[u][0][0];
+    for (int u = 0; u < QT; ++u) {
+      // mask keys past the sequence and (causal) keys after the query: key k0 + off(t, v) + 4h
+      // is dropped when off(t, v) > lim, off(t, v) = 32t + 8(v/4) + v%4 a constant per register
+      if ((k0 + BK > S) || (a.causal && k0 + BK - 1 > qw + 32 * u)) {
+        const int qi = qw + 32 * u + qc;
+        const int last = a.causal && qi < S - 1 ? qi : S - 1;  // last visible key
+        const int lim = last - k0 - 4 * h;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) bm = fmaxf(bm, sc[u][t][v]);
-        // the two halves of the wave hold the same queries: exchange without LDS
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), false, false);
-        bm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
-        // both halves see the same bm and mc, so they take the same decision
-        if (__builtin_amdgcn_ballot_w64(bm > mc[u] + RESCALE) != 0) {
-          const float mn = fmaxf(mc[u], bm);
-          const float corr = __builtin_amdgcn_exp2f(mc[u] - mn);
-          mc[u] = mn;
-          l[u] *= corr;
-#pragma unroll
-          for (int t = 0; t < DTL; ++t)
-#pragma unroll
-            for (int v = 0; v < 16; ++v) o[u][t][v] *= corr;
-        }
+          for (int v = 0; v < 16; ++v)
+            if (t * 32 + (v >> 2) * 8 + (v & 3) > lim) sc[u][t][v] = -INFINITY;
       }
-      // S^T of block kb+1 (its K is already in LDS) interleaved with the exponentials of block kb
-      // wave priority: the section that interleaves the next S^T MFMAs with this block's softmax
-      // goes first when both waves of a SIMD are ready (measured 3 % faster than equal priority)
-      __builtin_amdgcn_s_setprio(1);
-      s_mfma(kbuf(P ^ 1), sn);
+      float bm = sc[u][0][0];
 #pragma unroll
-      for (int u = 0; u < QT; ++u) {
-        // the row sum adds the rounded probabilities (the ones the P.V product uses), two at a
-        // time with v_dot2 against (1, 1), in two chains
-        float rs[2] = {0.f, 0.f};
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int v = 0; v < 16; ++v) bm = fmaxf(bm, sc[u][t][v]);
+      // the two halves of the wave hold the same queries: exchange without LDS
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), false, false);
+      bm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
+      // both halves see the same bm and mc, so they take the same decision
+      if (__builtin_amdgcn_ballot_w64(bm > mc[u] + RESCALE) != 0) {
+        const float mn = fmaxf(mc[u], bm);
+        const float corr = __builtin_amdgcn_exp2f(mc[u] - mn);
+        mc[u] = mn;
+        l[u] *= corr;
 #pragma unroll
-          for (int v2 = 0; v2 < 8; ++v2) {
-            const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[u][t][2 * v2], c, -mc[u]));
-            const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[u][t][2 * v2 + 1], c, -mc[u]));
-            const uint32_t pp = pack2<DT>(p0, p1);
-            rs[v2 & 1] = sum2<DT>(pp, rs[v2 & 1]);
-            // step s = 2t + v2/4 takes v = 8*(s%2) .. +7 of tile t
-            pf[u][2 * t + (v2 >> 2)][v2 & 3] = pp;
-          }
-        l[u] += rs[0] + rs[1];
+        for (int t = 0; t < DTL; ++t)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[u][t][v] *= corr;
       }
-      // O^T += V^T . P^T for block kb. V^T fragments come straight from the row-major V block
-      // with ds_read_b64_tr_b16: in each 16-lane group, input lane 4k'+q points at key row k',
-      // dims 4q..4q+3, and output lane i receives keys 0..3 of dim i. Two reads fetch exactly the
-      // key groups the probability registers hold: 16s + 4h + 0..3 and 16s + 8 + 4h + 0..3.
-      __builtin_amdgcn_s_setprio(0);
-      const KU_LDS unsigned char* LV = vbuf(P);
-      const int g = lane >> 4, c16 = lane & 15;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int t = 0; t < DTL; ++t) {
-          const int d = t * 32 + (g & 1) * 16 + (c16 & 3) * 4;
-          u32x2 half[2];
-#pragma unroll
-          for (int r2 = 0; r2 < 2; ++r2) {
-            const int kr = 16 * s + 8 * r2 + 4 * h + (c16 >> 2);
-            const KU_LDS unsigned char* p = LV + kr * RB + (((d >> 3) ^ vswz(kr)) << 4) + (d & 7) * 2;
-            half[r2] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KU_LDS s16x4*)p));
-          }
-          const u32x4 vf = u32x4{half[0][0], half[0][1], half[1][0], half[1][1]};
-#pragma unroll
-          for (int u = 0; u < QT; ++u) o[u][t] = mfma<DT>(vf, pf[u][s], o[u][t]);
-        }
     }
-    // this thread's DMA for the next blocks has landed; the barrier publishes it
+    // S^T of the next block (its K is already in LDS) interleaved with the exponentials of block
+    // kb. Wave priority: the section that interleaves the next S^T MFMAs with this block's softmax
+    // goes first when both waves of a SIMD are ready (measured 3 % faster than equal priority)
+    __builtin_amdgcn_s_setprio(1);
+    s_mfma(kbuf(P ^ 1), sn);
+#pragma unroll
+    for (int u = 0; u < QT; ++u) {
+      // the row sum adds the rounded probabilities (the ones the P.V product uses), two at a
+      // time with v_dot2 against (1, 1), in two chains
+      float rs[2] = {0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int v2 = 0; v2 < 8; ++v2) {
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[u][t][2 * v2], c, -mc[u]));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[u][t][2 * v2 + 1], c, -mc[u]));
+          const uint32_t pp = pack2<DT>(p0, p1);
+          rs[v2 & 1] = sum2<DT>(pp, rs[v2 & 1]);
+          // step s = 2t + v2/4 takes v = 8*(s%2) .. +7 of tile t
+          pf[u][2 * t + (v2 >> 2)][v2 & 3] = pp;
+        }
+      l[u] += rs[0] + rs[1];
+    }
+    // O^T += V^T . P^T for block kb. V^T fragments come straight from the row-major V block
+    // with ds_read_b64_tr_b16: in each 16-lane group, input lane 4k'+q points at key row k',
+    // dims 4q..4q+3, and output lane i receives keys 0..3 of dim i. Two reads fetch exactly the
+    // key groups the probability registers hold: 16s + 4h + 0..3 and 16s + 8 + 4h + 0..3.
+    __builtin_amdgcn_s_setprio(0);
+    const KU_LDS unsigned char* LV = vbuf(P);
+    const int g = lane >> 4, c16 = lane & 15;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < DTL; ++t) {
+        const int d = t * 32 + (g & 1) * 16 + (c16 & 3) * 4;
+        u32x2 half[2];
+#pragma unroll
+        for (int r2 = 0; r2 < 2; ++r2) {
+          const int kr = 16 * s + 8 * r2 + 4 * h + (c16 >> 2);
+          const KU_LDS unsigned char* p = LV + kr * RB + (((d >> 3) ^ vswz(kr)) << 4) + (d & 7) * 2;
+          half[r2] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KU_LDS s16x4*)p));
+        }
+        const u32x4 vf = u32x4{half[0][0], half[0][1], half[1][0], half[1][1]};
+#pragma unroll
+        for (int u = 0; u < QT; ++u) o[u][t] = mfma<DT>(vf, pf[u][s], o[u][t]);
+      }
+    // the S^T just issued was this tile's last: the Q fragments now belong to the next tile
+    if (kb + 2 == C.nkb) load_q(N);
+    // this thread's loads for the next blocks have landed; the barrier publishes them
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
   };
+
+  // the first tile's prologue: Q, K0, V0, K1 and the first scores
   f32x16 sa[QT][2], sb[QT][2];
+  load_q(C);
+  dma(kp, C.head, C.nkv, 0, kbuf(0), false);
+  dma(vp, C.head, C.nkv, 0, vbuf(0), true);
+  dma(kp, C.head, C.nkv, 1, kbuf(1), false);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
   s_mfma(kbuf(0), sa);
-  for (int kb = 0; kb < nkb; kb += 2) {
-    block(kb, sa, sb, std::integral_constant<int, 0>{});
-    if (kb + 1 < nkb) block(kb + 1, sb, sa, std::integral_constant<int, 1>{});
-  }
-
+  __syncthreads();  // block 0 refills K buffer 0: every wave has read it
+  for (;;) {
 #pragma unroll
-  for (int u = 0; u < QT; ++u) {
-    const int64_t qi = qw + 32 * u + qc;
-    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l[u]), __float_as_uint(l[u]), false, false);
-    const float lt = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
-    if (qi >= S) continue;
-    const float inv = 1.f / lt;
-    uint16_t* O = static_cast<uint16_t*>(a.o) + base + qi * D;
+    for (int u = 0; u < QT; ++u) {
+      mc[u] = -INFINITY;
+      l[u] = 0.f;
 #pragma unroll
-    for (int t = 0; t < DTL; ++t)
+      for (int t = 0; t < DTL; ++t)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = t * 32 + g * 8 + h * 4;
-        u32x2 w;
-        w[0] = pack2<DT>(o[u][t][4 * g] * inv, o[u][t][4 * g + 1] * inv);
-        w[1] = pack2<DT>(o[u][t][4 * g + 2] * inv, o[u][t][4 * g + 3] * inv);
-        *reinterpret_cast<u32x2*>(O + d0) = w;
+        for (int v = 0; v < 16; ++v) o[u][t][v] = 0.f;
+    }
+    for (int kb = 0; kb < C.nkb; kb += 2) {
+      block(kb, sa, sb, std::integral_constant<int, 0>{});
+      block(kb + 1, sb, sa, std::integral_constant<int, 1>{});
+    }
+    // Epilogue: normalise, then stage through V buffer 1 (free between a tile's last block and
+    // the next tile's first DMA; each wave owns 4 KB = 32 queries x 64 dims, 16-byte chunks
+    // swizzled by row) so every store writes whole 128-byte lines: eight rows of 16 lanes x 16
+    // bytes per instruction instead of 8-byte pieces of 32 rows, whose drain through the memory
+    // pipeline stalled the next tile's first instructions.
+    static_assert(QT == 1 && DTL % 2 == 0, "epilogue staging");
+    {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(l[0]), __float_as_uint(l[0]), false, false);
+      const float inv = 1.f / (__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+      KU_LDS unsigned char* R = vbuf(1) + wave * 4096;
+      uint16_t* Oh = static_cast<uint16_t*>(a.o) + C.head * HS;
+#pragma unroll
+      for (int hf = 0; hf < DTL / 2; ++hf) {
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            // lane (qc, h) holds dims 32t + 8g + 4h .. +3 of query qc: chunk 4tt + g, bytes 8h..
+            const f32x16& ot = o[0][2 * hf + tt];
+            u32x2 w;
+            w[0] = pack2<DT>(ot[4 * g] * inv, ot[4 * g + 1] * inv);
+            w[1] = pack2<DT>(ot[4 * g + 2] * inv, ot[4 * g + 3] * inv);
+            *(KU_LDS u32x2*)(R + qc * 128 + (((4 * tt + g) ^ (qc & 7)) << 4) + 8 * h) = w;
+          }
+        // one wave writes and reads its own region: its LDS operations complete in order
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int qr = (lane >> 3) + 8 * i, cc = lane & 7;
+          const u32x4 val = *(const KU_LDS u32x4*)(R + qr * 128 + ((cc ^ (qr & 7)) << 4));
+          if (qw + qr < S) *reinterpret_cast<u32x4*>(Oh + (int64_t)(qw + qr) * D + hf * 64 + cc * 8) = val;
+        }
       }
+      // every wave's staging reads are done before the next tile's first DMA refills V buffer 1
+      // (a bare barrier: the stores need not have completed)
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
+    if (N.nkb == 0) break;
+    C = N;
+    N = tile_at(++round + 1);
+    qw = C.q0 + wave * QW;
   }
-}
-
-int attn_qt() {
-  static const int q = [] {
-    const char* e = std::getenv("KURUMI_HIP_ATTN_QT");
-    return (e && e[0] == '2') ? 2 : 1;
-  }();
-  return q;
 }
 
 template <int D, int DT>
 void launch_d(const AttnArgs& a, hipStream_t s) {
-  constexpr int NW = 4;
-  if (attn_qt() == 2) {
-    const int64_t nqt = (a.s + 64 * NW - 1) / (64 * NW);
-    hipLaunchKernelGGL((attn_mfma_k<D, DT, NW, 2>), dim3((unsigned)(nqt * a.bh)), dim3(NW * 64), 0, s, a);
-  } else {
-    const int64_t nqt = (a.s + 32 * NW - 1) / (32 * NW);
-    hipLaunchKernelGGL((attn_mfma_k<D, DT, NW, 1>), dim3((unsigned)(nqt * a.bh)), dim3(NW * 64), 0, s, a);
-  }
+  constexpr int NW = 4, BQ = 32 * NW;
+  const int64_t ntiles = (a.s + BQ - 1) / BQ * a.bh;
+  // two resident work-groups per CU; KURUMI_HIP_ATTN_GRID caps the grid (tests use it to give
+  // every work-group several tiles at small shapes)
+  int64_t g = std::min<int64_t>(ntiles, 2 * (int64_t)cu_count());
+  if (const char* e = std::getenv("KURUMI_HIP_ATTN_GRID"); e && *e && std::atoll(e) > 0)
+    g = std::min<int64_t>(g, std::atoll(e));
+  if (g < ntiles) g = std::max<int64_t>(8, g & ~int64_t(7));  // mirrored rounds need whole XCD groups
+  hipLaunchKernelGGL((attn_mfma_k<D, DT, NW>), dim3((unsigned)g), dim3(NW * 64), 0, s, a);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }

@@ -410,16 +410,6 @@ void launch_tile(const GemmArgs& a, hipStream_t s) {
     hipLaunchKernelGGL((gemm_lds_k<E, BNMAJ, OT, BM, BN, WM, WN, false, OCC>), grid, dim3(WM * WN * 64), 0, s, a);
 }
 
-int cu_count() {
-  static const int n = [] {
-    int dev = 0, c = 0;
-    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
-      c = 256;
-    return c;
-  }();
-  return n;
-}
-
 // One work-group per CU at a time (the stages fill the LDS), so the tiles run in rounds of
 // cu_count(). 192-row tiles win when they need no more rounds than 256-row ones by enough to
 // outweigh their ~10 % lower efficiency (a 96 x 64 wave tile reads more LDS per MFMA): measured
@@ -461,6 +451,16 @@ void launch_e(const GemmArgs& a, hipStream_t s) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 }  // namespace
+
+int cu_count() {
+  static const int n = [] {
+    int dev = 0, c = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0)
+      c = 256;
+    return c;
+  }();
+  return n;
+}
 
 bool gemm_lds_ok(const GemmArgs& a) {
   if (const char* e = std::getenv("KURUMI_HIP_NO_MFMA"); e && *e && *e != '0') return false;

@@ -29,6 +29,9 @@ struct GemmArgs {
   int round_type = -1;
 };
 
+// Compute units of the current device (cached on first use): sizes persistent grids and tile rounds.
+int cu_count();
+
 // Short name of the kernel variant that will run (for plan labels): the MFMA kernel's element
 // type, layout and tile ("gemm_mfma_bf16_nn_256x256"; "_a64" when an operand spans 2^31 bytes or
 // more and the 64-bit-address DMA form runs), or "gemm_generic".

@@ -216,6 +216,25 @@ def test_attention_dtypes_and_non_causal_match_oracle(hip, dt, causal, s):
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="attention")
 
 
+@pytest.mark.parametrize("grid", ["8", "16"])
+@pytest.mark.parametrize("dt,causal,shape", [(DType.BF16, True, [2, 4, 300, 128]), (DType.BF16, False, [2, 4, 192, 128]),
+                                             (DType.F16, True, [1, 8, 520, 64]), (DType.BF16, False, [3, 3, 130, 64]),
+                                             (DType.BF16, True, [1, 9, 64, 128])])
+def test_attention_persistent_work_groups_match_oracle(hip, monkeypatch, grid, dt, causal, shape):
+    # a capped grid gives every work-group several q-tiles in a row (mirrored rounds, tiles of
+    # different lengths, odd key-block counts padded to even, partial last tiles), so the
+    # pipeline that runs across tile boundaries is checked against the oracle at small shapes
+    print(f"attention persistent grid={grid} dt={dt} causal={causal} shape={shape}", flush=True)
+    monkeypatch.setenv("KURUMI_HIP_ATTN_GRID", grid)
+    g, q, k, v, o = attention_graph(shape, dt, causal, True)
+    mk = f16_tensor if dt == DType.F16 else bf16_tensor
+    feeds = {q: mk(randn(shape, 61)), k: mk(randn(shape, 62)), v: mk(randn(shape, 63))}
+    assert "attn_mfma" in hip.plan(g, [o], feeds).steps()[0]
+    got = to_f32(hip.eval_with(g, o, feeds))
+    want = to_f32(interpret(g, [o], feeds)[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="attention")
+
+
 def test_attention_full_size_mfma_agrees_with_rowwise_kernel(hip, monkeypatch):
     # cfg 4 at its real shape: the MFMA flash kernel against the independent one-query-per-thread
     # kernel (f32 dot products, no MFMA), which the small-shape tests pin to the oracle
