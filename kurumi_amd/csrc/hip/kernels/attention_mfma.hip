@@ -30,6 +30,7 @@
 #include <type_traits>
 
 #include "kernels.h"
+#include "lds_dma.h"
 #include "numeric.h"
 
 namespace ku::hipbk {
@@ -211,7 +212,7 @@ attn_mfma_k(AttnArgs a) {
     for (int i = 0; i < NBLK; ++i) {
       const int blk = i * NW + wave, r = blk * (1024 / RB) + lane / CPR, pc = lane % CPR;
       const int cc = pc ^ (isv ? vswz(r) : kswz(r));
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(R, (KU_LDS void*)(wd + i * NW * 1024), 16, r * RB + cc * 16, 0, 0, 0);
+      lds_dma16(R, r * RB + cc * 16, 0, (KU_LDS void*)(wd + i * NW * 1024));
     }
   };
   auto kbuf = [&](int i) { return lds + i * TBYTES; };
@@ -340,7 +341,7 @@ attn_mfma_k(AttnArgs a) {
     // the S^T just issued was this tile's last: the Q fragments now belong to the next tile
     if (kb + 2 == C.nkb) load_q(N);
     // this thread's loads for the next blocks have landed; the barrier publishes them
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    vm_wait<0>();
     __syncthreads();
   };
 
@@ -350,7 +351,7 @@ attn_mfma_k(AttnArgs a) {
   dma(kp, C.head, C.nkv, 0, kbuf(0), false);
   dma(vp, C.head, C.nkv, 0, vbuf(0), true);
   dma(kp, C.head, C.nkv, 1, kbuf(1), false);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  vm_wait<0>();
   __syncthreads();
   s_mfma(kbuf(0), sa);
   __syncthreads();  // block 0 refills K buffer 0: every wave has read it

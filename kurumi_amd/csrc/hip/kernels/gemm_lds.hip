@@ -20,11 +20,14 @@
 // B columns in its L2. Semantics: kurumi_core/src/interp/contract.rs:26-64.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "kernels.h"
+#include "lds_dma.h"
 #include "numeric.h"
 
 namespace ku::hipbk {
@@ -38,6 +41,9 @@ typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef short s16x4 __attribute__((__vector_size__(4 * sizeof(short))));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 #define KU_LDS __attribute__((address_space(3)))
 
 enum Elem : int { E_BF16 = 0, E_F16 = 1, E_FP8 = 2 };
@@ -82,6 +88,15 @@ struct Op<E_FP8> {
   }
 };
 
+// two f32 -> one dword of two 16-bit floats, round to nearest even, in one packed conversion
+// (v_cvt_pk_bf16_f32 / the f16 pair form) rather than a conversion, shift and or per value
+template <int OT>
+__device__ __forceinline__ uint32_t pack_out(float lo, float hi) {
+  const f32x2 v = {lo, hi};
+  if constexpr (OT == GT_BF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+  else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
+}
+
 template <int OT>
 __device__ __forceinline__ void store_out(void* c, int64_t idx, float v) {
   if constexpr (OT == GT_BF16) static_cast<uint16_t*>(c)[idx] = d_bf16_st(v);
@@ -104,9 +119,7 @@ __device__ __forceinline__ void tile_of(int pid, int tm, int tn, int* im, int* i
   *in = r / gs;
 }
 
-__device__ __forceinline__ void dma16(const void* g, KU_LDS unsigned char* l) {
-  __builtin_amdgcn_global_load_lds(g, (KU_LDS void*)l, 16, 0, 0);
-}
+__device__ __forceinline__ void dma16(const void* g, KU_LDS unsigned char* l) { lds_dma16_g(g, (KU_LDS void*)l); }
 // Buffer-resource form of the same DMA: a per-lane 32-bit offset that stays fixed across stages
 // plus the stage's uniform offset in an SGPR (no 64-bit per-lane address arithmetic per stage;
 // measured 9 % faster on the cfg 3 GEMM). Used when every operand byte lies within 2^31 of the
@@ -116,7 +129,7 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* p) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff, 0x00020000);
 }
 __device__ __forceinline__ void bdma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, KU_LDS unsigned char* l) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (KU_LDS void*)l, 16, voff, soff, 0, 0);
+  lds_dma16(r, voff, soff, (KU_LDS void*)l);
 }
 
 template <int E, bool BNMAJ, int OT, int BM, int BN, int WM, int WN, bool BUF, int OCC>
@@ -253,7 +266,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
   };
 
   if (KT > 0) issue(0, 0);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  vm_wait<0>();
   __syncthreads();
   for (int kt = 0; kt < KT; ++kt) {
     const int cur = kt & 1;
@@ -298,7 +311,7 @@ __global__ void __launch_bounds__(WM* WN * 64)
       }
     }
     // this thread's DMA for stage kt+1 has landed; the barrier publishes it and retires stage kt
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    vm_wait<0>();
     __syncthreads();
   }
 
@@ -312,15 +325,32 @@ __global__ void __launch_bounds__(WM* WN * 64)
   void* C = static_cast<unsigned char*>(a.c) + bz * a.m * a.n * (OT == GT_F32 ? 4 : 2);
   const int64_t rbase = m0 + wm * TM, cbase = n0 + wn * TN;
   float cs[FN][4][4];  // column scales of this lane's columns
+  if (a.col_scale) {
+    // one uniform branch around all loads, so they are issued back to back and waited for once
+    // (a test per element put each load in its own block, waited for on its own)
 #pragma unroll
-  for (int j = 0; j < FN; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int64_t col = cbase + j * 32 + g * 8 + h * 4 + e;
-        cs[j][g][e] = a.col_scale ? alpha * a.col_scale[(col < a.n ? col : a.n - 1) * a.col_scale_stride] : alpha;
-      }
+        for (int e = 0; e < 4; ++e) {
+          const int64_t col = cbase + j * 32 + g * 8 + h * 4 + e;
+          cs[j][g][e] = a.col_scale[(col < a.n ? col : a.n - 1) * a.col_scale_stride];
+        }
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cs[j][g][e] *= alpha;
+  } else {
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) cs[j][g][e] = alpha;
+  }
   if constexpr (OT != GT_F32) {
     constexpr int ROWB = TN * 2;          // bytes per staged row
     constexpr int UPR = ROWB / 8;         // 8-byte units per row
@@ -343,13 +373,8 @@ __global__ void __launch_bounds__(WM* WN * 64)
             for (int e = 0; e < 4; ++e) v[e] = d_round_through(rt, v[e]);
           }
           u32x2 w;
-          if constexpr (OT == GT_BF16) {
-            w[0] = (uint32_t)d_bf16_st(v[0]) | ((uint32_t)d_bf16_st(v[1]) << 16);
-            w[1] = (uint32_t)d_bf16_st(v[2]) | ((uint32_t)d_bf16_st(v[3]) << 16);
-          } else {
-            w[0] = (uint32_t)d_f16_st(v[0]) | ((uint32_t)d_f16_st(v[1]) << 16);
-            w[1] = (uint32_t)d_f16_st(v[2]) | ((uint32_t)d_f16_st(v[3]) << 16);
-          }
+          w[0] = pack_out<OT>(v[0], v[1]);
+          w[1] = pack_out<OT>(v[2], v[3]);
           *(KU_LDS u32x2*)(EP + r * ROWB + ((u ^ ((r >> 1) & 15)) << 3)) = w;
         }
     }
@@ -388,6 +413,229 @@ __global__ void __launch_bounds__(WM* WN * 64)
             if (col + e < a.n)
               static_cast<float*>(C)[row * a.n + col + e] = d_round_through(rt, acc[i][j][4 * g + e] * cs[j][g][e]);
         }
+    }
+  }
+}
+
+// Persistent small-K GEMM (K of one or two 128-byte stages, e.g. the batched [8, 2048, 128] x
+// [8, 128, 2048] product): C is the traffic (K = 128 writes 8x the bytes it reads), so the kernel
+// is built to keep C stores streaming. One work-group of 8 waves per CU takes a contiguous run of
+// 128 x 128 tiles in (batch, tile row, tile column) order, so consecutive tiles share their A
+// rows: A is loaded once per tile row, B (all K stages) two tiles ahead into a ring of three LDS
+// buffers. The waves specialise. Waves 0-3 ("loaders") issue every DMA and multiply (a 64 x 64
+// block each); waves 4-7 ("storers") write C. A CU's vector memory requests are served in order,
+// so under streaming stores a load takes microseconds: the two tiles of lead hide that, and since
+// a wave's memory operations also retire in issue order, keeping the stores in other waves lets
+// the loaders wait for their loads alone (the storers never wait). Per tile t, between two
+// barriers the loaders park tile t - 1's results in a staging buffer, start B of tile t + 2 and
+// wait for tile t's operands; after the second barrier they multiply tile t while the storers
+// read tile t - 1 back from the staging buffer and store whole 128-byte row segments. Rows or
+// columns past C go to an out-of-range buffer offset (dropped).
+__device__ __forceinline__ void bar_lds() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int E, bool BNMAJ, int OT, int KT>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) gemm_smallk_k(GemmArgs a) {
+  constexpr int BM = 128, BN = 128, WM = 2, WN = 2, NL = WM * WN;  // NL loader waves, then NL storers
+  constexpr int EB = 2, KE = KB / EB;
+  constexpr int TM = BM / WM, TN = BN / WN, FM = TM / 32, FN = TN / 32;
+  constexpr int KSTEP = Op<E>::KSTEP, LV = Op<E>::LV, NKS = KB / KSTEP;
+  constexpr int SA = BM * KB, SB = BN * KB;          // one stage of A, of B (16 KB each)
+  constexpr int ABUF = KT * SA, BBUF = KT * SB;      // a tile's A, B (all stages)
+  constexpr int NB = 3;                              // B ring: the current tile and two ahead
+  constexpr int ROWB = TN * 2;                       // bytes of one staged row of a loader's block
+  constexpr int BLK = TM * ROWB;                     // one loader's staged block
+  constexpr int STG = NL * BLK;                      // the staging buffer: the whole C tile
+  constexpr int AIL = SA / 1024 / NL, BIL = SB / 1024 / NL;  // 1 KB DMA blocks per loader wave
+  constexpr int NROW = BN * 2, NCH = NROW / 16, NRPB = 1024 / NROW;
+  constexpr int LB = KT * BIL;           // B DMA operations per loader wave per tile
+  constexpr int SPB = BLK / 1024;        // store operations per storer per tile
+  static_assert(E != E_FP8 && OT != GT_F32 && TM == 64 && TN == 64 && ROWB == 128, "small-K layout");
+  static_assert(AIL * NL * 1024 == SA && BIL * NL * 1024 == SB && NRPB * NROW == 1024, "stage / wave mismatch");
+  static_assert(2 * LB <= 63 && STG == BM * BN * 2, "counters / staging");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds_raw[ABUF + NB * BBUF + STG];
+  KU_LDS unsigned char* lds = (KU_LDS unsigned char*)lds_raw;
+  KU_LDS unsigned char* LA = lds;
+  KU_LDS unsigned char* LS = lds + ABUF + NB * BBUF;
+  auto bbuf = [&](int slot) { return lds + ABUF + slot * BBUF; };
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), h = lane >> 5,
+            l32 = lane & 31;
+  const bool loader = wave < NL;
+  const int lw = loader ? wave : wave - NL;  // index within the role
+  const int wm = lw / WN, wn = lw % WN;
+  const int tm = (int)((a.m + BM - 1) / BM), tn = (int)((a.n + BN - 1) / BN);
+  const int ntile = tm * tn * (int)a.batch;
+  const int per = (ntile + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int t0 = (int)blockIdx.x * per, t1 = min(ntile, t0 + per);
+  if (t0 >= t1) return;  // the whole work-group
+  const auto RC = __builtin_amdgcn_make_buffer_rsrc(a.c, (short)0, (int)(a.batch * a.m * a.n * 2), 0x00020000);
+  const int rt = a.round_type;
+
+  // tile t: batch t / (tm tn), tile row (t / tn) % tm, tile column t % tn; its A depends on t / tn
+  auto load_a = [&](int t) {  // loader waves
+    const int bz = t / (tm * tn);
+    const int64_t m0 = (int64_t)((t / tn) % tm) * BM;
+    const auto RA = gemm_rsrc(static_cast<const unsigned char*>(a.a) + bz * a.sab * EB);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int i = 0; i < AIL; ++i) {
+        const int blk = i * NL + lw, r = blk * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+        const int64_t gm = m0 + r < a.m ? m0 + r : a.m - 1;
+        bdma16(RA, (uint32_t)(gm * a.sam * EB + c * 16 + kt * KB), 0, LA + kt * SA + blk * 1024);
+      }
+  };
+  auto load_b = [&](int t, int slot) {  // loader waves
+    const int bz = t / (tm * tn);
+    const int64_t n0 = (int64_t)(t % tn) * BN;
+    const auto RBs = gemm_rsrc(static_cast<const unsigned char*>(a.b) + bz * a.sbb * EB);
+    KU_LDS unsigned char* base = bbuf(slot);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int i = 0; i < BIL; ++i) {
+        const int blk = i * NL + lw;
+        uint32_t off;
+        if constexpr (!BNMAJ) {
+          const int r = blk * 8 + (lane >> 3), c = (lane & 7) ^ ((r >> 1) & 7);
+          const int64_t gn = n0 + r < a.n ? n0 + r : a.n - 1;
+          off = (uint32_t)(gn * a.sbn * EB + c * 16 + kt * KB);
+        } else {
+          const int r = blk * NRPB + lane / NCH, c = (lane % NCH) ^ (4 * (r & 3));
+          const int64_t gn = n0 + c * 8 < a.n ? n0 + c * 8 : a.n - 8;
+          off = (uint32_t)((((int64_t)kt * KE + r) * a.sbk + gn) * 2);
+        }
+        bdma16(RBs, off, 0, base + kt * SB + blk * 1024);
+      }
+  };
+
+  f32x16 acc[FM][FN];
+  // loader waves: the products of tile t into acc
+  auto compute = [&](int slot) {
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+    const KU_LDS unsigned char* LB0 = bbuf(slot);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        u32x4 fa[FM][LV], fb[FN][LV];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int r = wm * TM + i * 32 + l32;
+#pragma unroll
+          for (int v = 0; v < LV; ++v) {
+            const int c = ks * (KSTEP / 16) + h * LV + v;
+            fa[i][v] = *(const KU_LDS u32x4*)(LA + kt * SA + r * KB + ((c ^ ((r >> 1) & 7)) << 4));
+          }
+        }
+        const KU_LDS unsigned char* Lb = LB0 + kt * SB;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) {
+          if constexpr (!BNMAJ) {
+            const int r = wn * TN + j * 32 + l32;
+#pragma unroll
+            for (int v = 0; v < LV; ++v) {
+              const int c = ks * (KSTEP / 16) + h * LV + v;
+              fb[j][v] = *(const KU_LDS u32x4*)(Lb + r * KB + ((c ^ ((r >> 1) & 7)) << 4));
+            }
+          } else {
+            const int g = lane >> 4, c16 = lane & 15;
+            const int n = wn * TN + j * 32 + (g & 1) * 16 + (c16 & 3) * 4;
+            u32x2 hv[2];
+#pragma unroll
+            for (int r2 = 0; r2 < 2; ++r2) {
+              const int k = ks * 16 + (g >> 1) * 8 + r2 * 4 + (c16 >> 2);
+              const KU_LDS unsigned char* p = Lb + k * NROW + (((n >> 3) ^ (4 * (k & 3))) << 4) + (n & 7) * 2;
+              hv[r2] = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((KU_LDS s16x4*)p));
+            }
+            fb[j][0] = u32x4{hv[0][0], hv[0][1], hv[1][0], hv[1][1]};
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) Op<E>::run(acc[i][j], fb[j], fa[i]);
+      }
+  };
+  // loader waves: acc into this wave's block of the staging buffer. C^T tiles: lane l32 owns row
+  // i*32 + l32 and, in register group g of tile j, the 4 columns j*32 + 8g + 4h + 0..3; 8-byte
+  // unit u of row r sits at u ^ ((r/2) % 16)
+  auto stage = [&](auto round) __attribute__((always_inline)) {
+    KU_LDS unsigned char* EP = LS + lw * BLK;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int r = i * 32 + l32;
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int u = j * 8 + g * 2 + h;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            v[e] = decltype(round)::value ? d_round_through(rt, acc[i][j][4 * g + e]) : acc[i][j][4 * g + e];
+          u32x2 w;
+          w[0] = pack_out<OT>(v[0], v[1]);
+          w[1] = pack_out<OT>(v[2], v[3]);
+          *(KU_LDS u32x2*)(EP + r * ROWB + ((u ^ ((r >> 1) & 15)) << 3)) = w;
+        }
+    }
+  };
+  // storer waves: read back loader lw's block of tile t and store it
+  auto store = [&](int t) {
+    const int bz = t / (tm * tn);
+    const int64_t rbase = (int64_t)((t / tn) % tm) * BM + wm * TM, cbase = (int64_t)(t % tn) * BN + wn * TN;
+    const KU_LDS unsigned char* EP = LS + lw * BLK;
+#pragma unroll
+    for (int q = 0; q < SPB; ++q) {
+      const int r = q * 8 + (lane >> 3), c = lane & 7, sw = (r >> 1) & 15;
+      const u32x2 lo = *(const KU_LDS u32x2*)(EP + r * ROWB + (((2 * c) ^ sw) << 3));
+      const u32x2 hi = *(const KU_LDS u32x2*)(EP + r * ROWB + (((2 * c + 1) ^ sw) << 3));
+      const int64_t row = rbase + r, col = cbase + c * 8;
+      // n % 8 == 0: a chunk is wholly inside or outside C
+      const uint32_t off = row < a.m && col < a.n ? (uint32_t)((bz * a.m * a.n + row * a.n + col) * 2) : 0x80000000u;
+      __builtin_amdgcn_raw_buffer_store_b128(u32x4{lo[0], lo[1], hi[0], hi[1]}, RC, off, 0, 0);
+    }
+  };
+
+  if (loader) {
+    load_a(t0);
+    load_b(t0, 0);
+    if (t0 + 1 < t1) load_b(t0 + 1, 1);
+  }
+  for (int t = t0, slot = 0; t <= t1; ++t, slot = slot == NB - 1 ? 0 : slot + 1) {
+    // tile t - 1 is multiplied (every loader) and tile t - 2 read back from staging (every storer)
+    bar_lds();
+    if (loader) {
+      if (t > t0) {
+        if (rt >= 0) stage(std::true_type{});
+        else stage(std::false_type{});
+      }
+      if (t < t1) {
+        if (t > t0 && t / tn != (t - 1) / tn) {
+          // a new tile row: tile t - 1 no longer needs A; reload it and wait for everything
+          load_a(t);
+          vm_wait<0>();
+        }
+        // B of tile t + 2 goes where tile t - 1's B was
+        if (t + 2 < t1) load_b(t + 2, slot == 0 ? 2 : slot - 1);
+        // tile t's operands; at most the B loads of tiles t + 1 and t + 2 were issued after them
+        if (t + 2 < t1) vm_wait<2 * LB>();
+        else if (t + 1 < t1) vm_wait<LB>();
+        else vm_wait<0>();
+      }
+    }
+    // tile t's operands and tile t - 1's staged results are in place
+    bar_lds();
+    if (loader) {
+      if (t < t1) compute(slot);
+    } else if (t > t0) {
+      store(t - 1);
     }
   }
 }
@@ -432,8 +680,30 @@ bool small_k(const GemmArgs& a) {
   return kbytes <= 2 * 128;
 }
 
+// the persistent small-K kernel: 16-bit operands and output, no scales, whole 16-byte output
+// chunks, 32-bit offsets into every operand and into C
+bool smallk_persistent(const GemmArgs& a) {
+  if (!small_k(a) || a.in_type == GT_F8E4M3 || a.out_type == GT_F32 || a.alpha || a.col_scale) return false;
+  if (a.n % 8 || !spans_fit(a) || a.batch * a.m * a.n * 2 >= (int64_t(1) << 31)) return false;
+  return (a.m + 127) / 128 * ((a.n + 127) / 128) * a.batch < (int64_t(1) << 30);
+}
+
+template <int E, bool BNMAJ, int OT>
+void launch_smallk(const GemmArgs& a, hipStream_t s) {
+  const int64_t tiles = (a.m + 127) / 128 * ((a.n + 127) / 128) * a.batch;
+  // one work-group per CU; KURUMI_HIP_SMALLK_GRID caps the grid (the tests use it to give every
+  // work-group several tiles at small shapes)
+  int64_t g = std::min<int64_t>(tiles, cu_count());
+  if (const char* e = std::getenv("KURUMI_HIP_SMALLK_GRID"); e && *e && std::atoll(e) > 0) g = std::min<int64_t>(g, std::atoll(e));
+  if (a.k * 2 <= 128) hipLaunchKernelGGL((gemm_smallk_k<E, BNMAJ, OT, 1>), dim3((unsigned)g), dim3(512), 0, s, a);
+  else hipLaunchKernelGGL((gemm_smallk_k<E, BNMAJ, OT, 2>), dim3((unsigned)g), dim3(512), 0, s, a);
+}
+
 template <int E, bool BNMAJ, int OT>
 void launch_cfg(const GemmArgs& a, hipStream_t s) {
+  if constexpr (E != E_FP8 && OT != GT_F32) {
+    if (smallk_persistent(a)) return launch_smallk<E, BNMAJ, OT>(a, s);
+  }
   if (small_k(a)) launch_tile<E, BNMAJ, OT, 128, 128, 2, 2, 2>(a, s);
   else if (rows192(a)) launch_tile<E, BNMAJ, OT, 192, 256, 2, 4>(a, s);
   else launch_tile<E, BNMAJ, OT, 256, 256, 2, 4>(a, s);
@@ -485,7 +755,7 @@ bool gemm_lds_ok(const GemmArgs& a) {
 std::string gemm_lds_name(const GemmArgs& a) {
   std::string n = a.in_type == GT_F8E4M3 ? "gemm_mfma_e4m3" : a.in_type == GT_F16 ? "gemm_mfma_f16" : "gemm_mfma_bf16";
   n += a.sbk == 1 ? "_nt" : "_nn";
-  n += small_k(a) ? "_128x128" : rows192(a) ? "_192x256" : "_256x256";
+  n += smallk_persistent(a) ? "_128x128_persistent" : small_k(a) ? "_128x128" : rows192(a) ? "_192x256" : "_256x256";
   if (!spans_fit(a)) n += "_a64";
   return n;
 }

@@ -54,7 +54,7 @@ def test_cfg3_gemm_steps():
     assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn_256x256 b1 m4096 n11008 k4096"]
     g = Graph()
     c = g.dot_general(g.input([8, 2048, 128], DType.BF16), g.input([8, 128, 2048], DType.BF16), [2], [1], [0], [0])
-    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn_128x128 b8 m2048 n2048 k128"]
+    assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nn_128x128_persistent b8 m2048 n2048 k128"]
     g = Graph()
     c = g.dot_general(g.input([64, 256], DType.BF16), g.input([128, 256], DType.BF16), [1], [1])
     assert steps(g.codegen([c])) == ["gemm_mfma_bf16_nt_192x256 b1 m64 n128 k256"]

@@ -112,7 +112,7 @@ def test_cfg3_bench_plan_full_size(hip):
 def test_cfg3b_bench_plan_full_size(hip):
     print("cfg3b bench plan [8,2048,128]@[8,128,2048]", flush=True)
     c = bench.make_gemm(hip, batched=True)
-    assert c.plan.steps() == ["gemm_mfma_bf16_nn_128x128 b8 m2048 n2048 k128"]
+    assert c.plan.steps() == ["gemm_mfma_bf16_nn_128x128_persistent b8 m2048 n2048 k128"]
     c.plan.launch()
     got = to_f32(c.plan.output(0))
     truth = np.matmul(bf16_f64(c.feeds[c.a]), bf16_f64(c.feeds[c.b]))

@@ -498,3 +498,25 @@ def test_scaled_fp8_dot_square_output_matches_oracle(hip, per_row):
     got = to_f32(hip.eval_with(g, y, feeds))
     want = to_f32(interpret(g, [y], feeds)[0])
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what=f"scaled fp8 dot per_row={per_row}")
+
+
+@pytest.mark.parametrize("grid", ["3", "16"])
+@pytest.mark.parametrize("dt,nt,b,m,k,n", [(DType.BF16, False, 3, 300, 128, 264), (DType.F16, True, 2, 257, 64, 392),
+                                           (DType.BF16, True, 5, 128, 64, 136), (DType.F16, False, 1, 520, 128, 128)])
+def test_small_k_gemm_persistent_work_groups_match_oracle(hip, monkeypatch, grid, dt, nt, b, m, k, n):
+    # K of one or two 128-byte stages runs on the persistent small-K kernel; a capped grid gives
+    # every work-group several tiles in a row (buffer alternation, the waits that let the next
+    # tile's loads overtake the previous tile's stores, tiles cut by M and N), checked against
+    # the oracle
+    print(f"small-K gemm grid={grid} {dt.name} nt={nt} {b}x{m}x{k}x{n}", flush=True)
+    monkeypatch.setenv("KURUMI_HIP_SMALLK_GRID", grid)
+    g = Graph()
+    a = g.input([b, m, k], dt)
+    w = g.input([b, n, k] if nt else [b, k, n], dt)
+    c = g.dot_general(a, w, [2], [2] if nt else [1], [0], [0])
+    mk = f16_tensor if dt == DType.F16 else bf16_tensor
+    feeds = {a: mk(randn([b, m, k], 37, 1.0 / 8)), w: mk(randn([b, n, k] if nt else [b, k, n], 38, 1.0 / 8))}
+    assert "_persistent" in hip.plan(g, [c], feeds).steps()[0]
+    got = to_f32(hip.eval_with(g, c, feeds))
+    want = to_f32(interpret(g, [c], feeds)[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="small-K gemm")
