@@ -296,24 +296,43 @@ attn_mfma_k(AttnArgs a) {
     // kb. Wave priority: the section that interleaves the next S^T MFMAs with this block's softmax
     // goes first when both waves of a SIMD are ready (measured 3 % faster than equal priority)
     __builtin_amdgcn_s_setprio(1);
-    s_mfma(kbuf(P ^ 1), sn);
-#pragma unroll
-    for (int u = 0; u < QT; ++u) {
+    {
+      // The 2*DS S^T MFMAs of the next block (MFMA m: k-step m/2, key tile m%2) interleaved with
+      // the 16 exponential pairs of this block (16 / (2*DS) pairs before each MFMA), each K
+      // fragment read two MFMAs ahead; a scheduling barrier after each group keeps the compiler
+      // from regrouping them (left to itself it ran the MFMAs back to back, each waiting for its
+      // own LDS read, and the softmax after them).
+      constexpr int NM = 2 * DS, PPM = 16 / NM;
+      static_assert(NM * PPM == 16, "exponential pairs per MFMA");
+      const KU_LDS unsigned char* LK = kbuf(P ^ 1);
+      auto kread = [&](int m) {
+        const int r = (m & 1) * 32 + qc;
+        return *(const KU_LDS u32x4*)(LK + r * RB + (((2 * (m >> 1) + h) ^ kswz(r)) << 4));
+      };
       // the row sum adds the rounded probabilities (the ones the P.V product uses), two at a
       // time with v_dot2 against (1, 1), in two chains
       float rs[2] = {0.f, 0.f};
+      u32x4 kf[3];
+      kf[0] = kread(0);
+      kf[1] = kread(1);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int m = 0; m < NM; ++m) {
+        if (m + 2 < NM) kf[(m + 2) % 3] = kread(m + 2);
 #pragma unroll
-        for (int v2 = 0; v2 < 8; ++v2) {
-          const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[u][t][2 * v2], c, -mc[u]));
-          const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[u][t][2 * v2 + 1], c, -mc[u]));
+        for (int e = 0; e < PPM; ++e) {
+          const int i = m * PPM + e, te = i >> 3, v2 = i & 7;
+          const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[0][te][2 * v2], c, -mc[0]));
+          const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[0][te][2 * v2 + 1], c, -mc[0]));
           const uint32_t pp = pack2<DT>(p0, p1);
           rs[v2 & 1] = sum2<DT>(pp, rs[v2 & 1]);
           // step s = 2t + v2/4 takes v = 8*(s%2) .. +7 of tile t
-          pf[u][2 * t + (v2 >> 2)][v2 & 3] = pp;
+          pf[0][2 * te + (v2 >> 2)][v2 & 3] = pp;
         }
-      l[u] += rs[0] + rs[1];
+        // the first k-step of each key tile starts from zero
+        sn[0][m & 1] = mfma<DT>(kf[m % 3], qf[0][m >> 1], m < 2 ? f32x16{} : sn[0][m & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      l[0] += rs[0] + rs[1];
     }
     // O^T += V^T . P^T for block kb. V^T fragments come straight from the row-major V block
     // with ds_read_b64_tr_b16: in each 16-lane group, input lane 4k'+q points at key row k',
