@@ -84,7 +84,7 @@ def _declare(L: C.CDLL) -> None:
         "ku_graph_free": ([P], None),
         "ku_input": ([P, psz, sz, u32], u32),
         "ku_constant_f32": ([P, C.POINTER(C.c_float), sz, psz, sz], u32),
-        "ku_constant": ([P, u32, C.c_char_p, sz, psz, sz], u32),
+        "ku_constant": ([P, u32, C.c_void_p, sz, psz, sz], u32),
         "ku_scalar": ([P, u32, C.c_float], u32),
         "ku_where": ([P, u32, u32, u32], u32),
         "ku_clamp_min": ([P, u32, C.c_float], u32),
@@ -128,7 +128,7 @@ def _declare(L: C.CDLL) -> None:
         "ku_feeds_free": ([P], None),
         "ku_feeds_set": ([P, u32, P], None),
         "ku_tensor_f32": ([C.POINTER(C.c_float), sz, psz, sz], P),
-        "ku_tensor_new": ([u32, C.c_char_p, sz, psz, sz], P),
+        "ku_tensor_new": ([u32, C.c_void_p, sz, psz, sz], P),
         "ku_tensor_free": ([P], None),
         "ku_tensor_rank": ([P], sz),
         "ku_tensor_shape": ([P, psz], None),
@@ -136,7 +136,7 @@ def _declare(L: C.CDLL) -> None:
         "ku_tensor_dtype": ([P], u32),
         "ku_tensor_data_f32": ([P, C.POINTER(C.c_float), sz], C.c_ssize_t),
         "ku_tensor_nbytes": ([P], sz),
-        "ku_tensor_bytes": ([P, C.c_char_p], None),
+        "ku_tensor_bytes": ([P, C.c_void_p], None),
         "ku_hip_plan_new": ([P, C.POINTER(C.c_uint32), sz, P, P], P),
         "ku_hip_plan_feed": ([P, u32, P], C.c_int32),
         "ku_hip_plan_launch": ([P, u32], C.c_int32),
@@ -212,10 +212,27 @@ def _check_node(n: int, what: str) -> int:
     return n
 
 
-class Tensor:
-    """Owned host tensor (the reference's `TensorVal`): dtype, shape, raw LE bytes."""
+def _raw(data):
+    """(pointer, byte length) of a tensor's storage: `bytes`/`bytearray`, or a C-contiguous
+    numpy array (the storage of tensors that came back from the library)."""
+    if isinstance(data, np.ndarray):
+        if not data.flags.c_contiguous:
+            raise KuError("tensor storage must be C-contiguous")
+        return (data.ctypes.data if data.nbytes else None), data.nbytes
+    if isinstance(data, bytearray):
+        return (C.addressof(C.c_char.from_buffer(data)) if data else None), len(data)
+    return bytes(data), len(data)
 
-    def __init__(self, dtype: DType, shape: Sequence[int], data: bytes):
+
+class Tensor:
+    """Owned host tensor (the reference's `TensorVal`): dtype, shape, raw LE bytes.
+
+    `data` is `bytes` for tensors built here and a flat `uint8` numpy array for tensors
+    returned by the library (one copy out of the C handle instead of three); both expose the
+    buffer protocol and `len()` in bytes.
+    """
+
+    def __init__(self, dtype: DType, shape: Sequence[int], data):
         self.dtype = DType(dtype)
         self.shape = tuple(int(x) for x in shape)
         self.data = data
@@ -244,7 +261,8 @@ class Tensor:
 
     def _handle(self):
         s, r = _shape(self.shape)
-        h = lib().ku_tensor_new(int(self.dtype), self.data, len(self.data), s, r)
+        ptr, n = _raw(self.data)
+        h = lib().ku_tensor_new(int(self.dtype), ptr, n, s, r)
         if not h:
             raise KuError(f"ku_tensor_new: {last_error()}")
         return h
@@ -256,9 +274,10 @@ class Tensor:
         shp = (C.c_size_t * max(r, 1))()
         L.ku_tensor_shape(h, shp)
         n = L.ku_tensor_nbytes(h)
-        buf = C.create_string_buffer(max(n, 1))
-        L.ku_tensor_bytes(h, buf)
-        t = Tensor(DType(L.ku_tensor_dtype(h)), list(shp)[:r], buf.raw[:n])
+        buf = np.empty(n, np.uint8)
+        if n:
+            L.ku_tensor_bytes(h, buf.ctypes.data)
+        t = Tensor(DType(L.ku_tensor_dtype(h)), list(shp)[:r], buf)
         L.ku_tensor_free(h)
         return t
 
@@ -299,11 +318,13 @@ class Graph:
     def constant(self, data: np.ndarray, dtype: DType | None = None) -> int:
         t = Tensor.from_numpy(np.asarray(data), dtype)
         s, r = _shape(t.shape)
-        return self._n("ku_constant", int(t.dtype), t.data, len(t.data), s, r)
+        ptr, n = _raw(t.data)
+        return self._n("ku_constant", int(t.dtype), ptr, n, s, r)
 
-    def constant_bytes(self, dtype: DType, raw: bytes, shape: Sequence[int]) -> int:
+    def constant_bytes(self, dtype: DType, raw, shape: Sequence[int]) -> int:
         s, r = _shape(shape)
-        return self._n("ku_constant", int(dtype), raw, len(raw), s, r)
+        ptr, n = _raw(raw)
+        return self._n("ku_constant", int(dtype), ptr, n, s, r)
 
     def scalar(self, like: int, v: float) -> int:
         return self._n("ku_scalar", like, float(v))

@@ -343,7 +343,7 @@ void ku_backend_free(KuBackend* b) { delete b; }
 
 static KuTensor* eval_impl(KuGraph* g, KuNode node, const KuBackend* b, const ku::Feeds& f) {
   auto outs = b->b->eval_many(g->g, {node}, f);
-  return new KuTensor{std::move(outs[0])};
+  return new_ku_tensor(std::move(outs[0]));
 }
 
 KuTensor* ku_eval(KuGraph* g, KuNode node, const KuBackend* backend) {
@@ -369,7 +369,7 @@ int32_t ku_eval_many(KuGraph* g, const KuNode* ids, size_t n, const KuBackend* b
   return guard<int32_t>(-1, [&] {
     std::vector<NodeId> v(ids, ids + n);
     auto outs = backend->b->eval_many(g->g, v, feeds->f);
-    for (size_t i = 0; i < outs.size(); ++i) out[i] = new KuTensor{std::move(outs[i])};
+    for (size_t i = 0; i < outs.size(); ++i) out[i] = new_ku_tensor(std::move(outs[i]));
     return 0;
   });
 }
@@ -445,7 +445,7 @@ KuTensor* ku_plan_run(const KuPlan* p, const KuGraph* g, const KuFeeds* feeds) {
       throw ku::Error("ku_plan_run: the plan was compiled on a different graph");
     ku::hipbk::feed_plan(*p->p, feeds->f);
     p->p->launch(true);
-    return new KuTensor{p->p->download(0)};
+    return new_ku_tensor(p->p->download(0));
   });
 }
 void ku_plan_free(KuPlan* p) { delete p; }
@@ -456,7 +456,7 @@ KuFeeds* ku_feeds_new(void) { return new KuFeeds(); }
 void ku_feeds_free(KuFeeds* f) { delete f; }
 void ku_feeds_set(KuFeeds* f, KuNode node, const KuTensor* t) {
   if (!f || !t) return;
-  f->f[node] = std::make_shared<ku::Tensor>(t->t);
+  f->f[node] = t->t;  // shared, not copied
 }
 
 KuTensor* ku_tensor_f32(const float* data, size_t len, const size_t* shape, size_t rank) {
@@ -464,11 +464,11 @@ KuTensor* ku_tensor_f32(const float* data, size_t len, const size_t* shape, size
     if (!data && len) throw ku::Error("ku_tensor_f32: null data");  // capi/tensor.rs:57-60
     Shape s = mk_shape(shape, rank);
     if (ku::numel(s) != len) throw ku::Error("ku_tensor_f32: len does not match shape");
-    auto* t = new KuTensor();
-    t->t.dtype = ku::DType::F32;
-    t->t.shape = s;
-    t->t.bytes.resize(len * 4);
-    if (len) std::memcpy(t->t.bytes.data(), data, len * 4);
+    ku::Tensor x;
+    x.dtype = ku::DType::F32;
+    x.shape = s;
+    x.bytes.assign(reinterpret_cast<const uint8_t*>(data), reinterpret_cast<const uint8_t*>(data) + len * 4);
+    auto* t = new_ku_tensor(std::move(x));
     return t;
   });
 }
@@ -478,37 +478,38 @@ KuTensor* ku_tensor_new(uint32_t dtype, const uint8_t* data, size_t nbytes, cons
     ku::DType dt = to_dt(dtype);
     Shape s = mk_shape(shape, rank);
     if (ku::numel(s) * ku::dt_width(dt) != nbytes) throw ku::Error("ku_tensor_new: nbytes does not match shape");
-    auto* t = new KuTensor();
-    t->t.dtype = dt;
-    t->t.shape = s;
-    t->t.bytes.assign(data, data + nbytes);
+    ku::Tensor x;
+    x.dtype = dt;
+    x.shape = s;
+    x.bytes.assign(data, data + nbytes);
+    auto* t = new_ku_tensor(std::move(x));
     return t;
   });
 }
 void ku_tensor_free(KuTensor* t) { delete t; }
-size_t ku_tensor_rank(const KuTensor* t) { return t ? t->t.shape.size() : 0; }
+size_t ku_tensor_rank(const KuTensor* t) { return t ? t->t->shape.size() : 0; }
 void ku_tensor_shape(const KuTensor* t, size_t* out) {
-  if (t && out) std::memcpy(out, t->t.shape.data(), t->t.shape.size() * sizeof(size_t));
+  if (t && out) std::memcpy(out, t->t->shape.data(), t->t->shape.size() * sizeof(size_t));
 }
-size_t ku_tensor_len(const KuTensor* t) { return t ? ku::numel(t->t.shape) : 0; }
-uint32_t ku_tensor_dtype(const KuTensor* t) { return t ? static_cast<uint32_t>(t->t.dtype) : KU_ERR; }
+size_t ku_tensor_len(const KuTensor* t) { return t ? ku::numel(t->t->shape) : 0; }
+uint32_t ku_tensor_dtype(const KuTensor* t) { return t ? static_cast<uint32_t>(t->t->dtype) : KU_ERR; }
 ptrdiff_t ku_tensor_data_f32(const KuTensor* t, float* out, size_t cap) {
   if (!t || !out) return -1;
-  if (t->t.dtype != ku::DType::F32) {
+  if (t->t->dtype != ku::DType::F32) {
     set_err("ku_tensor_data_f32: tensor is not F32");
     return -1;
   }
-  size_t n = ku::numel(t->t.shape);
+  size_t n = ku::numel(t->t->shape);
   if (cap < n) {
     set_err("ku_tensor_data_f32: buffer too small");
     return -1;
   }
-  std::memcpy(out, t->t.bytes.data(), n * 4);
+  std::memcpy(out, t->t->bytes.data(), n * 4);
   return static_cast<ptrdiff_t>(n);
 }
-size_t ku_tensor_nbytes(const KuTensor* t) { return t ? t->t.bytes.size() : 0; }
+size_t ku_tensor_nbytes(const KuTensor* t) { return t ? t->t->bytes.size() : 0; }
 void ku_tensor_bytes(const KuTensor* t, uint8_t* out) {
-  if (t && out && !t->t.bytes.empty()) std::memcpy(out, t->t.bytes.data(), t->t.bytes.size());
+  if (t && out && !t->t->bytes.empty()) std::memcpy(out, t->t->bytes.data(), t->t->bytes.size());
 }
 
 // ---------------- device-resident plans ----------------
@@ -535,7 +536,7 @@ KuHipPlan* ku_hip_plan_new(KuGraph* g, const KuNode* roots, size_t n, const KuBa
 int32_t ku_hip_plan_feed(KuHipPlan* p, KuNode input, const KuTensor* t) {
   if (!p || !t) return -1;
   return guard<int32_t>(-1, [&] {
-    p->p->feed(input, t->t);
+    p->p->feed(input, *t->t);
     return 0;
   });
 }
@@ -555,7 +556,7 @@ int32_t ku_hip_plan_sync(KuHipPlan* p) {
 }
 KuTensor* ku_hip_plan_output(KuHipPlan* p, size_t i) {
   if (!p) return nullptr;
-  return guard<KuTensor*>(nullptr, [&] { return new KuTensor{p->p->download(i)}; });
+  return guard<KuTensor*>(nullptr, [&] { return new_ku_tensor(p->p->download(i)); });
 }
 size_t ku_hip_plan_num_steps(const KuHipPlan* p) { return p ? p->p->num_steps() : 0; }
 size_t ku_hip_plan_step_label(const KuHipPlan* p, size_t i, char* out, size_t cap) {

@@ -20,7 +20,7 @@ int32_t kuo_interpret(const KuGraph* g, const uint32_t* roots, size_t n, const K
     ku::Feeds empty;
     std::vector<ku::NodeId> r(roots, roots + n);
     auto res = kuo::interpret(g->g, r, feeds ? feeds->f : empty);
-    for (size_t i = 0; i < n; ++i) out[i] = new KuTensor{std::move(res[i])};
+    for (size_t i = 0; i < n; ++i) out[i] = new_ku_tensor(std::move(res[i]));
     return 0;
   } catch (const std::exception& e) {
     g_err = e.what();
@@ -36,12 +36,12 @@ int32_t kuo_realize(const KuGraph* g, uint32_t root, const KuFeeds* feeds, KuTen
     ku::Tensor t;
     int p = 0;
     if (kuo::realize(g->g, root, feeds ? feeds->f : empty, &t, &p)) {
-      *out = new KuTensor{std::move(t)};
+      *out = new_ku_tensor(std::move(t));
       if (passes) *passes = p;
       return 1;
     }
     auto res = kuo::interpret(g->g, {root}, feeds ? feeds->f : empty);
-    *out = new KuTensor{std::move(res[0])};
+    *out = new_ku_tensor(std::move(res[0]));
     if (passes) *passes = -1;
     return 0;
   } catch (const std::exception& e) {
