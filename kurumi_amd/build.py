@@ -56,7 +56,7 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")
     _run([f"{ROCM}/bin/hipcc", "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-          f"-L{ROCM}/lib", "-lhiprtc", "-lamdhip64", f"-Wl,-rpath,{ROCM}/lib"])
+          f"-L{ROCM}/lib", "-lhiprtc", "-lamdhip64", "-pthread", f"-Wl,-rpath,{ROCM}/lib"])
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")

@@ -15,6 +15,7 @@
 #include "errors.h"
 #include "handles.h"
 #include "../ir/graph.h"
+#include "../ir/hostcopy.h"
 #include "../ir/quant.h"
 #include "../ir/tensor.h"
 
@@ -467,7 +468,9 @@ KuTensor* ku_tensor_f32(const float* data, size_t len, const size_t* shape, size
     ku::Tensor x;
     x.dtype = ku::DType::F32;
     x.shape = s;
-    x.bytes.assign(reinterpret_cast<const uint8_t*>(data), reinterpret_cast<const uint8_t*>(data) + len * 4);
+    x.bytes.resize(len * 4);
+    ku::advise_huge(x.bytes.data(), x.bytes.size());
+    ku::par_copy(x.bytes.data(), data, len * 4);
     auto* t = new_ku_tensor(std::move(x));
     return t;
   });
@@ -481,7 +484,9 @@ KuTensor* ku_tensor_new(uint32_t dtype, const uint8_t* data, size_t nbytes, cons
     ku::Tensor x;
     x.dtype = dt;
     x.shape = s;
-    x.bytes.assign(data, data + nbytes);
+    x.bytes.resize(nbytes);
+    ku::advise_huge(x.bytes.data(), nbytes);
+    ku::par_copy(x.bytes.data(), data, nbytes);
     auto* t = new_ku_tensor(std::move(x));
     return t;
   });
@@ -504,12 +509,12 @@ ptrdiff_t ku_tensor_data_f32(const KuTensor* t, float* out, size_t cap) {
     set_err("ku_tensor_data_f32: buffer too small");
     return -1;
   }
-  std::memcpy(out, t->t->bytes.data(), n * 4);
+  ku::par_copy(out, t->t->bytes.data(), n * 4);
   return static_cast<ptrdiff_t>(n);
 }
 size_t ku_tensor_nbytes(const KuTensor* t) { return t ? t->t->bytes.size() : 0; }
 void ku_tensor_bytes(const KuTensor* t, uint8_t* out) {
-  if (t && out && !t->t->bytes.empty()) std::memcpy(out, t->t->bytes.data(), t->t->bytes.size());
+  if (t && out && !t->t->bytes.empty()) ku::par_copy(out, t->t->bytes.data(), t->t->bytes.size());
 }
 
 // ---------------- device-resident plans ----------------

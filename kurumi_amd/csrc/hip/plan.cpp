@@ -1,6 +1,7 @@
 // Fusion planner + plan executor for the HIP backend (see plan.h).
 #include "plan.h"
 
+#include "../ir/hostcopy.h"
 #include "fingerprint.h"
 
 #include <algorithm>
@@ -229,7 +230,7 @@ std::shared_ptr<ConstEntry> ConstCache::get(const Graph& g, NodeId id) {
   e->pool = &ctx_->pool();
   e->nbytes = e->buf.bytes;
   e->last_use = ++clock_;
-  if (nb) KU_HIP(hipMemcpyAsync(e->buf.ptr, n.op.data->data(), nb, hipMemcpyHostToDevice, ctx_->stream()));
+  if (nb) ctx_->upload(e->buf.ptr, n.op.data->data(), nb);
   uploads_++;
   by_content_[key] = e;
   enforce_budget();
@@ -1774,7 +1775,7 @@ void Plan::feed(NodeId input, const Tensor& t) {
   if (t.bytes.size() != s.bytes) throw Error("feed: byte size mismatch");
   if (!s.bytes) return;
   if (debug_enabled()) std::fprintf(stderr, "[kurumi_hip] feed %%%u -> %p (%zu bytes)\n", input, s.buf.ptr, s.bytes);
-  KU_HIP(hipMemcpyAsync(s.buf.ptr, t.bytes.data(), s.bytes, hipMemcpyHostToDevice, ctx_->stream()));
+  ctx_->upload(s.buf.ptr, t.bytes.data(), s.bytes);
   ctx_->profile().launches[(int)Kind::Upload]++;
 }
 
@@ -1915,10 +1916,9 @@ Tensor Plan::download(size_t i) {
   Tensor t;
   t.dtype = root_meta_.at(i).first;
   t.shape = root_meta_.at(i).second;
-  t.bytes.resize(numel(t.shape) * dt_width(t.dtype));
-  if (!t.bytes.empty())
-    KU_HIP(hipMemcpyAsync(t.bytes.data(), slots_[rv.first].buf.ptr, t.bytes.size(), hipMemcpyDeviceToHost,
-                          ctx_->stream()));
+  t.bytes.resize(numel(t.shape) * dt_width(t.dtype));  // left uninitialised: the copy writes every byte
+  advise_huge(t.bytes.data(), t.bytes.size());
+  if (!t.bytes.empty()) ctx_->download(t.bytes.data(), slots_[rv.first].buf.ptr, t.bytes.size());
   ctx_->sync();
   ctx_->profile().launches[(int)Kind::Download]++;
   return t;

@@ -1,9 +1,12 @@
 #include "runtime.h"
 
+#include "../ir/hostcopy.h"
+
 #include <hip/hiprtc.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -196,7 +199,79 @@ Context::~Context() {
   if (stream_) {
     (void)hipSetDevice(device_);
     (void)hipStreamSynchronize(stream_);
+    for (int i = 0; i < 2; ++i) {
+      if (stage_ev_[i]) (void)hipEventDestroy(stage_ev_[i]);
+      if (stage_[i]) (void)hipHostFree(stage_[i]);
+    }
     (void)hipStreamDestroy(stream_);
+  }
+}
+
+namespace {
+constexpr size_t kStageChunk = size_t(32) << 20;
+// Below this a pageable copy's fixed cost is lower than the staging loop's.
+constexpr size_t kStageMin = size_t(4) << 20;
+}  // namespace
+
+bool Context::ensure_stage() {
+  if (stage_[1]) return true;
+  if (stage_failed_) return false;
+  for (int i = 0; i < 2; ++i) {
+    if (hipHostMalloc(&stage_[i], kStageChunk, hipHostMallocDefault) != hipSuccess) {
+      (void)hipGetLastError();
+      for (int j = 0; j <= i; ++j) {
+        if (stage_[j]) (void)hipHostFree(stage_[j]);
+        stage_[j] = nullptr;
+      }
+      stage_failed_ = true;  // pinned memory unavailable: stay on pageable copies
+      return false;
+    }
+    KU_HIP(hipEventCreateWithFlags(&stage_ev_[i], hipEventDisableTiming));
+  }
+  return true;
+}
+
+void Context::upload(void* dev, const void* host, size_t n) {
+  if (!n) return;
+  if (n < kStageMin || !ensure_stage()) {
+    KU_HIP(hipMemcpyAsync(dev, host, n, hipMemcpyHostToDevice, stream_));
+    return;
+  }
+  for (size_t off = 0, c = 0; off < n; off += kStageChunk, ++c) {
+    const int b = int(c & 1);
+    const size_t len = std::min(kStageChunk, n - off);
+    if (stage_recorded_[b]) KU_HIP(hipEventSynchronize(stage_ev_[b]));  // its last DMA has read it
+    par_copy(stage_[b], static_cast<const uint8_t*>(host) + off, len);
+    KU_HIP(hipMemcpyAsync(static_cast<uint8_t*>(dev) + off, stage_[b], len, hipMemcpyHostToDevice, stream_));
+    KU_HIP(hipEventRecord(stage_ev_[b], stream_));
+    stage_recorded_[b] = true;
+  }
+}
+
+void Context::download(void* host, const void* dev, size_t n) {
+  if (!n) return;
+  if (n < kStageMin || !ensure_stage()) {
+    KU_HIP(hipMemcpyAsync(host, dev, n, hipMemcpyDeviceToHost, stream_));
+    sync();
+    return;
+  }
+  const size_t nc = (n + kStageChunk - 1) / kStageChunk;
+  auto issue = [&](size_t c) {
+    const int b = int(c & 1);
+    const size_t off = c * kStageChunk;
+    KU_HIP(hipMemcpyAsync(stage_[b], static_cast<const uint8_t*>(dev) + off, std::min(kStageChunk, n - off),
+                          hipMemcpyDeviceToHost, stream_));
+    KU_HIP(hipEventRecord(stage_ev_[b], stream_));
+    stage_recorded_[b] = true;
+  };
+  issue(0);
+  if (nc > 1) issue(1);
+  for (size_t c = 0; c < nc; ++c) {
+    const int b = int(c & 1);
+    const size_t off = c * kStageChunk;
+    KU_HIP(hipEventSynchronize(stage_ev_[b]));
+    par_copy(static_cast<uint8_t*>(host) + off, stage_[b], std::min(kStageChunk, n - off));
+    if (c + 2 < nc) issue(c + 2);
   }
 }
 

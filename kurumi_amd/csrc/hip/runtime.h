@@ -100,8 +100,16 @@ class Context {
   void make_current() const;
   bool timing() const { return timing_; }
   void set_timing(bool on) { timing_ = on; }
+  // Host <-> device copies of tensors crossing the C boundary. Large ones go in 32 MiB chunks
+  // through two pinned staging buffers (allocated on first use): the DMA runs at pinned rate
+  // and overlaps the multi-threaded host copy of the neighbouring chunk. upload() is ordered on
+  // the context stream and may return before its last DMA ends (the host buffer is free on
+  // return); download() returns with `host` filled.
+  void upload(void* dev, const void* host, size_t n);
+  void download(void* host, const void* dev, size_t n);
 
  private:
+  bool ensure_stage();
   int device_;
   hipStream_t stream_ = nullptr;
   Pool pool_;
@@ -110,6 +118,10 @@ class Context {
   std::string arch_;
   int num_cus_ = 0;
   bool timing_ = false;
+  void* stage_[2] = {nullptr, nullptr};
+  hipEvent_t stage_ev_[2] = {nullptr, nullptr};
+  bool stage_recorded_[2] = {false, false};
+  bool stage_failed_ = false;
 };
 
 }  // namespace ku::hipbk

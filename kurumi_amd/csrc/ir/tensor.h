@@ -3,6 +3,9 @@
 #pragma once
 #include <cstdint>
 #include <memory>
+#include <new>
+#include <type_traits>
+#include <utility>
 #include <unordered_map>
 #include <vector>
 
@@ -11,10 +14,27 @@
 
 namespace ku {
 
+// std::allocator that default-initialises (leaves uninitialised) the elements `resize` adds. A
+// tensor's bytes are always written whole by the copy that fills them, so value-initialising a
+// GB-sized download buffer first would be a wasted pass over host memory.
+template <class T>
+struct NoInitAlloc : std::allocator<T> {
+  template <class U>
+  struct rebind { using other = NoInitAlloc<U>; };
+  NoInitAlloc() noexcept = default;
+  template <class U>
+  NoInitAlloc(const NoInitAlloc<U>&) noexcept {}
+  template <class U>
+  void construct(U* p) noexcept(std::is_nothrow_default_constructible<U>::value) { ::new (static_cast<void*>(p)) U; }
+  template <class U, class... A>
+  void construct(U* p, A&&... a) { ::new (static_cast<void*>(p)) U(std::forward<A>(a)...); }
+};
+using Bytes = std::vector<uint8_t, NoInitAlloc<uint8_t>>;
+
 struct Tensor {
   DType dtype = DType::F32;
   Shape shape;
-  std::vector<uint8_t> bytes;
+  Bytes bytes;
   size_t nbytes() const { return bytes.size(); }
 };
 

@@ -686,7 +686,7 @@ Tensor eval_op(const Node& n, const std::vector<const Tensor*>& in) {
       Tensor t;
       t.dtype = op.data_dtype;
       t.shape = op.shape;
-      t.bytes = *op.data;
+      t.bytes.assign(op.data->begin(), op.data->end());
       return t;
     }
     case OpKind::Detach: return *in[0];

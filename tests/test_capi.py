@@ -157,6 +157,27 @@ def test_tensor_round_trip_and_f32_readout():
     assert not bad and b"nbytes" in L.ku_last_error()
 
 
+@pytest.mark.parametrize("nbytes", [(16 << 20) + 4 * 12345, (40 << 20) - 4 * 7, 4 * 8 * 3])
+def test_large_tensor_round_trip_is_bit_exact(nbytes):
+    # ku_tensor_new / ku_tensor_bytes split copies of 16 MiB and more across threads on page
+    # boundaries; every byte must land in place for ragged sizes too (and the small case stays
+    # on one memcpy)
+    n = nbytes // 4
+    x = np.random.default_rng(nbytes).integers(0, 2**32, n, dtype=np.uint32).view(np.float32)
+    t = Tensor(DType.F32, [n], x.tobytes())
+    back = Tensor._from_handle(t._handle())
+    assert isinstance(back.data, np.ndarray) and back.data.nbytes == nbytes
+    np.testing.assert_array_equal(back.numpy().view(np.uint32), x.view(np.uint32))
+    # a numpy-backed tensor feeds the C side as well as a bytes-backed one
+    again = Tensor._from_handle(back._handle())
+    np.testing.assert_array_equal(again.numpy().view(np.uint32), x.view(np.uint32))
+    buf = np.empty(n, np.float32)
+    h = back._handle()
+    assert K.lib().ku_tensor_data_f32(h, buf.ctypes.data_as(C.POINTER(C.c_float)), n) == n
+    K.lib().ku_tensor_free(h)
+    np.testing.assert_array_equal(buf.view(np.uint32), x.view(np.uint32))
+
+
 def test_scalar_constant_takes_the_tensor_dtype():
     # elementwise.rs:83-94: the scalar const is built directly in like's dtype
     g = Graph()

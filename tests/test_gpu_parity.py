@@ -404,6 +404,22 @@ def test_eval_many_matches_single_eval(hip, dt):
         np.testing.assert_array_equal(many[i].numpy(), one.numpy(), err_msg=f"output {i}")
 
 
+@pytest.mark.parametrize("n", [(96 << 20) // 4 + 12345, (8 << 20) // 4 + 3, (4 << 20) // 4 - 1])
+def test_large_feeds_and_downloads_are_bit_exact(hip, n):
+    # Feeds and results of 4 MiB and more cross the boundary in 32 MiB chunks through two pinned
+    # staging buffers: a ragged last chunk, a single partial chunk, and the pageable path below
+    # the staging threshold. Two evals in a row reuse the buffers; each must see its own input.
+    print(f"staged copies n={n}", flush=True)
+    g = Graph()
+    x = g.input([n], DType.F32)
+    y = g.add(x, g.scalar(x, 1.0))
+    for seed in (1, 2):
+        xv = np.random.default_rng(seed * n).standard_normal(n, dtype=np.float32)
+        got = hip.eval_many_with(g, [y, x], {x: Tensor.from_numpy(xv)})
+        np.testing.assert_array_equal(got[1].numpy().view(np.uint32), xv.view(np.uint32))
+        np.testing.assert_array_equal(got[0].numpy(), xv + np.float32(1.0))
+
+
 def test_missing_feed_is_an_error(hip):
     import kurumi_amd as K
 
