@@ -60,6 +60,7 @@ struct QuantArgs {
   const uint16_t* mins = nullptr;     // f16 [N, K / group], asymmetric only
   void* out = nullptr;                // [M, N] contiguous, act_type
   void* wdq = nullptr;                // dequantized weight [N, K] (wdq_type) for the GEMM path
+  void* mm_scratch = nullptr;         // quant_mm_scratch_bytes() of device scratch for the MFMA path
   int64_t m = 0, n = 0, k = 0, group = 0;
   int bits = 4;
   bool sym = true;
@@ -71,6 +72,10 @@ void launch_quant_gemv(const QuantArgs& a, hipStream_t s);
 void launch_quant_dequant(const QuantArgs& a, hipStream_t s);
 // fused dequant MFMA kernel: int4, bf16 / f16 act, 9 <= M <= 64, group a multiple of 64
 bool quant_mm_ok(const QuantArgs& a);
+// scratch of the MFMA path: act re-laid out in the order the kernel's lanes load it (whole lines
+// per load instruction) and its per-sub-group sums, written by one small pass shared by every
+// work-group
+size_t quant_mm_scratch_bytes(const QuantArgs& a);
 void launch_quant_mm(const QuantArgs& a, hipStream_t s);
 
 // Per-tensor e4m3 activation quantisation (linear_e4m3.hip): sx = max|x| * (1/448) and

@@ -410,8 +410,54 @@ __global__ void __launch_bounds__(256) quant_gemv_fast_k(QuantArgs a) {
 // j of the MFMA takes word 4h + j in half h (a permutation of k shared by both operands). A
 // work-group holds 32 * NT weight rows; its QMM_NW waves take the scale groups round-robin and
 // add their partials through LDS at the end. The rows' scales (and mins) are staged in LDS
-// transposed to [group][row] first.
+// transposed to [group][row] first. Act, the larger operand (every work-group reads all of it),
+// comes from quant_act_prep_k in the order the lanes load it: one load instruction reads 1 KB of
+// whole lines instead of 32 bytes from each of 32 rows.
 constexpr int QMM_NW = 8;
+
+// quant_mm_k's act operand, laid out for its loads. MP = 32 * MT rows (rows past M are zeros);
+// sub-group sg is GB blocks of 64 values. For block bb of sub-group sg, load q (0..3), row m and
+// lane half h, the 16 bytes at u32 index ((((sg * GB + bb) * 4 + q) * MP + m) * 2 + h) * 4 hold
+// the MFMA B operand of k-step q: pairs (value p, value p + 4), p = 0..3, of the 8 values at
+// k = 64 (sg GB + bb) + 32 h + 8 q. sums[(sg * MP + m) * 2 + h] is the v_dot2 chain of that
+// half's 32 GB values over the sub-group (the kernel adds the two halves).
+__host__ __device__ inline int64_t quant_act_rows(int64_t m) { return m <= 32 ? 32 : 64; }
+__host__ __device__ inline size_t quant_actp_bytes(int64_t m, int64_t k) {
+  return ((size_t)(quant_act_rows(m) * k * 2) + 255) & ~(size_t)255;
+}
+template <int AT, int GB>
+__global__ void __launch_bounds__(64) quant_act_prep_k(const uint16_t* __restrict__ act, uint32_t* __restrict__ actp,
+                                                       float* __restrict__ sums, int64_t m_rows, int64_t k) {
+  constexpr uint32_t ONES = AT == GT_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  constexpr uint32_t SEL[2] = {0x05040100u, 0x07060302u};  // v_perm_b32: half p of src1 | half p of src0
+  const int64_t mp = quant_act_rows(m_rows), nsg = k / (64 * GB);
+  const int64_t idx = (int64_t)blockIdx.x * 64 + threadIdx.x;  // (sg, m, h), h fastest
+  if (idx >= nsg * mp * 2) return;
+  const int h = (int)(idx & 1);
+  const int64_t m = (idx >> 1) % mp, sg = (idx >> 1) / mp;
+  // all of this thread's loads in flight at once (the pass is one memory latency long)
+  u32x4 v[GB][4];
+#pragma unroll
+  for (int bb = 0; bb < GB; ++bb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      v[bb][q] = m < m_rows ? *reinterpret_cast<const u32x4*>(act + m * k + (sg * GB + bb) * 64 + 32 * h + 8 * q)
+                            : u32x4{0, 0, 0, 0};
+  float as = 0.f;
+#pragma unroll
+  for (int bb = 0; bb < GB; ++bb)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) as = dot2<AT>(v[bb][q][i], ONES, as);
+      u32x4 o;
+#pragma unroll
+      for (int p = 0; p < 4; ++p) o[p] = __builtin_amdgcn_perm(v[bb][q][(p + 4) >> 1], v[bb][q][p >> 1], SEL[p & 1]);
+      *reinterpret_cast<u32x4*>(actp + ((((sg * GB + bb) * 4 + q) * mp + m) * 2 + h) * 4) = o;
+    }
+  sums[idx] = as;
+}
+
 template <bool SYM, int AT, int NT, int MT, int GB>
 __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
   typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -445,14 +491,15 @@ __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
     const int64_t n = n0 + 32 * t + l32;
     wrow[t] = a.qw + (n < N ? n : N - 1) * rb + 16 * h;
   }
-  const uint16_t* arow[MT];
-  bool alive[MT];
+  // the prepared act (quant_act_prep_k): this lane's 16 bytes of load q of block bb of sub-group sg
+  // at actp[(sg * GB + bb) * 4 + q][lane offset]; its sums at sums[sg][lane offset]
+  constexpr int MP = 32 * MT;
+  const uint32_t* actp = static_cast<const uint32_t*>(a.mm_scratch);
+  const float* sums = reinterpret_cast<const float*>(static_cast<const unsigned char*>(a.mm_scratch) +
+                                                     quant_actp_bytes(M, K));
+  int aoff[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int64_t m = 32 * mt + l32;
-    alive[mt] = m < M;
-    arow[mt] = static_cast<const uint16_t*>(a.act) + (m < M ? m : 0) * K + 32 * h;
-  }
+  for (int mt = 0; mt < MT; ++mt) aoff[mt] = (32 * mt + l32) * 2 + h;
   f32x16 acc[NT][MT];
 #pragma unroll
   for (int t = 0; t < NT; ++t)
@@ -476,7 +523,7 @@ __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const u32x4 v = alive[mt] ? *reinterpret_cast<const u32x4*>(arow[mt] + kb + 8 * q) : u32x4{0, 0, 0, 0};
+          const u32x4 v = *reinterpret_cast<const u32x4*>(actp + (((int64_t)(sg * GB + bb) * 4 + q) * MP * 2 + aoff[mt]) * 4);
 #pragma unroll
           for (int i = 0; i < 4; ++i) aw[bb][mt][4 * q + i] = v[i];
         }
@@ -486,26 +533,18 @@ __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
     f32x16 cg[NT][MT];
     float as[MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      as[mt] = 0.f;
-#pragma unroll
-      for (int bb = 0; bb < GB; ++bb)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) as[mt] = dot2<AT>(aw[bb][mt][i], ONES, as[mt]);
-    }
+    for (int mt = 0; mt < MT; ++mt) as[mt] = sums[(int64_t)sg * MP * 2 + aoff[mt]];
 #pragma unroll
     for (int bb = 0; bb < GB; ++bb)
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) {
-        // k-step jj of block bb: word 4h + jj of each row; act pairs (p, p + 4) of the same 8 values
+        // k-step jj of block bb: word 4h + jj of each row; act pairs (p, p + 4) of the same 8
+        // values, prepared in that order
         u32x4 bf[MT];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-          for (int p = 0; p < 4; ++p) {
-            constexpr uint32_t SEL[2] = {0x05040100u, 0x07060302u};
-            bf[mt][p] = __builtin_amdgcn_perm(aw[bb][mt][4 * jj + ((p + 4) >> 1)], aw[bb][mt][4 * jj + (p >> 1)], SEL[p & 1]);
-          }
+          for (int p = 0; p < 4; ++p) bf[mt][p] = aw[bb][mt][4 * jj + p];
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
           u32x4 af;
@@ -583,6 +622,16 @@ __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
 template <bool SYM, int AT, int NT, int MT>
 void launch_mm(const QuantArgs& a, hipStream_t s) {
   const int64_t ng = a.k / a.group;
+  {
+    const int gb = a.group % 128 == 0 ? 2 : 1;
+    const int64_t nthreads = a.k / (64 * gb) * quant_act_rows(a.m) * 2;
+    const dim3 pg((unsigned)((nthreads + 63) / 64));
+    const uint16_t* act = static_cast<const uint16_t*>(a.act);
+    uint32_t* actp = static_cast<uint32_t*>(a.mm_scratch);
+    float* sums = reinterpret_cast<float*>(static_cast<unsigned char*>(a.mm_scratch) + quant_actp_bytes(a.m, a.k));
+    if (gb == 2) hipLaunchKernelGGL((quant_act_prep_k<AT, 2>), pg, dim3(64), 0, s, act, actp, sums, a.m, a.k);
+    else hipLaunchKernelGGL((quant_act_prep_k<AT, 1>), pg, dim3(64), 0, s, act, actp, sums, a.m, a.k);
+  }
   const size_t lds = std::max<size_t>((size_t)ng * 32 * NT * 2 * (SYM ? 1 : 2), (size_t)QMM_NW * NT * MT * 16 * 64 * 4);
   const dim3 grid((unsigned)((a.n + 32 * NT - 1) / (32 * NT)));
   // sub-groups of two 64-value blocks when the scale group allows
@@ -705,10 +754,17 @@ bool quant_mm_ok(const QuantArgs& a) {
          (a.sym || a.mins);
 }
 
+size_t quant_mm_scratch_bytes(const QuantArgs& a) {
+  const int64_t nsg = a.k / (64 * (a.group % 128 == 0 ? 2 : 1));
+  return quant_actp_bytes(a.m, a.k) + (size_t)(nsg * quant_act_rows(a.m) * 2) * sizeof(float);
+}
+
 void launch_quant_mm(const QuantArgs& a, hipStream_t s) {
   check(a);
   if (!quant_mm_ok(a)) throw std::runtime_error("quant: shape not supported by the fused MFMA kernel");
   if (a.n == 0) return;
+  if (!a.mm_scratch || (reinterpret_cast<uintptr_t>(a.mm_scratch) & 15))
+    throw std::runtime_error("quant: the MFMA path needs a 16-byte aligned scratch of quant_mm_scratch_bytes()");
   if ((reinterpret_cast<uintptr_t>(a.qw) & 15) || (reinterpret_cast<uintptr_t>(a.act) & 15))
     throw std::runtime_error("quant: packed weight and act must be 16-byte aligned");
   if (a.sym) {

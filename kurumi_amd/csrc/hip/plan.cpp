@@ -1121,12 +1121,14 @@ void Planner::visit_quant(NodeId id) {
   Q.path = quant_gemv_ok(qa) ? QuantStep::GEMV : (quant_mm_ok(qa) ? QuantStep::MFMA : QuantStep::DEQUANT_GEMM);
   if (Q.path == QuantStep::DEQUANT_GEMM)
     Q.wdq_slot = new_slot(SlotKind::Temp, Q.wdq_dtype, Q.n * Q.k * dt_width(Q.wdq_dtype), id);
+  if (Q.path == QuantStep::MFMA) Q.mm_slot = new_slot(SlotKind::Temp, DType::U8, quant_mm_scratch_bytes(qa), id);
   P_.quants_.push_back(Q);
   int step = new_step(Step::QUANT, (int)P_.quants_.size() - 1, "quant");
   for (int i = 0; i < 4; ++i)
     if (slots[i] >= 0) depend(step, slots[i]);
   slot_producer_[Q.out_slot] = step;
   if (Q.wdq_slot >= 0) slot_producer_[Q.wdq_slot] = step;
+  if (Q.mm_slot >= 0) slot_producer_[Q.mm_slot] = step;
   Val v;
   v.k = Val::Dev;
   v.slot = Q.out_slot;
@@ -1854,6 +1856,7 @@ void Plan::launch_step(const Step& s) {
     if (Q.path == QuantStep::GEMV) {
       launch_quant_gemv(a, st);
     } else if (Q.path == QuantStep::MFMA) {
+      a.mm_scratch = slot_ptr(slots_, Q.mm_slot);
       launch_quant_mm(a, st);
     } else {
       a.wdq = slot_ptr(slots_, Q.wdq_slot);

@@ -122,7 +122,7 @@ struct GemmStep {
 struct QuantStep {
   enum Path { GEMV, MFMA, DEQUANT_GEMM };
   Path path = GEMV;
-  int act_slot = -1, qw_slot = -1, sc_slot = -1, mn_slot = -1, out_slot = -1, wdq_slot = -1;
+  int act_slot = -1, qw_slot = -1, sc_slot = -1, mn_slot = -1, out_slot = -1, wdq_slot = -1, mm_slot = -1;
   int64_t act_off = 0, qw_off = 0, sc_off = 0, mn_off = 0;  // elements
   size_t m = 0, n = 0, k = 0, group = 0;
   int bits = 4;
