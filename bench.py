@@ -423,13 +423,14 @@ def _cpu_line(value, unit, sample, reps, sec):
             "sample": f"{sample}; {reps} reps, {sec * 1e3:.1f} ms/rep; host nproc={os.cpu_count()}"}
 
 
-def cpu_baseline_cfg2(xt_full, rows_sample=256, cols=32000):
-    """The oracle interpreter on a row sample of the same logits (rows are independent)."""
+def cpu_baseline_cfg2(xt_full, rows_sample=1024, cols=32000):
+    """The oracle interpreter on a row sample of the same logits (rows are independent), about
+    10 s of single-core work."""
     kt, K = _oracle(), _ku()
     xs = np.ascontiguousarray(xt_full.numpy()[:rows_sample])
     g, x, y, a = softmax_graph(K, rows_sample, cols, K.DType.F32)
     feeds = {x: K.Tensor.from_numpy(xs)}
-    sec, reps = _time_cpu(lambda: kt.interpret(g, [y, a], feeds), 8.0)
+    sec, reps = _time_cpu(lambda: kt.interpret(g, [y, a], feeds), 10.0)
     algo_bytes = rows_sample * cols * 8 + rows_sample * 4
     return _cpu_line(round(algo_bytes / sec / 1e9, 4), "GB/s",
                      f"{rows_sample} of 8192 rows x 32000 f32, decomposed softmax + argmax via the oracle "
