@@ -61,6 +61,7 @@ struct QuantArgs {
   void* out = nullptr;                // [M, N] contiguous, act_type
   void* wdq = nullptr;                // dequantized weight [N, K] (wdq_type) for the GEMM path
   void* mm_scratch = nullptr;         // quant_mm_scratch_bytes() of device scratch for the MFMA path
+  bool qw_tiled = false;              // qw in the fused MFMA kernel's lane order (launch_quant_tile_weights)
   int64_t m = 0, n = 0, k = 0, group = 0;
   int bits = 4;
   bool sym = true;
@@ -76,6 +77,12 @@ bool quant_mm_ok(const QuantArgs& a);
 // per load instruction) and its per-sub-group sums, written by one small pass shared by every
 // work-group
 size_t quant_mm_scratch_bytes(const QuantArgs& a);
+// whether the MFMA path runs the fused kernel (groups a multiple of 128, operands under 2 GiB),
+// which needs no scratch and can read a weight held in its lane order
+bool quant_mm_fused_ok(const QuantArgs& a);
+// the lane-ordered copy of a packed int4 weight [n, k / 2]: bytes, and the pass that writes it
+size_t quant_tiled_bytes(int64_t n, int64_t k);
+void launch_quant_tile_weights(const uint8_t* qw, uint8_t* wt, int64_t n, int64_t k, hipStream_t s);
 void launch_quant_mm(const QuantArgs& a, hipStream_t s);
 
 // Per-tensor e4m3 activation quantisation (linear_e4m3.hip): sx = max|x| * (1/448) and

@@ -23,6 +23,7 @@
 #include <string>
 
 #include "kernels.h"
+#include "lds_dma.h"
 #include "numeric.h"
 
 namespace ku::hipbk {
@@ -619,6 +620,237 @@ __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_k(QuantArgs a) {
   }
 }
 
+#define KU_LDS __attribute__((address_space(3)))
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t qrsrc(const void* p, uint32_t bytes) {
+  // dword3 0x00020000: 32-bit data format, the raw-buffer setting for gfx9 parts
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// The fused MFMA kernel without the act pass (groups a multiple of 128, so every sub-group is two
+// 64-value blocks; operands under 2 GiB). Same products, sums and folds in the same order as
+// quant_mm_k, so the results are bit-identical; what changes is how the operands arrive. Each
+// wave streams its run of blocks through two LDS stage buffers by DMA (buffer_load ... lds), the
+// next block's DMAs in flight while the current block is computed:
+//   act: the block's 32 * MT rows x 128 bytes, 8 rows per DMA, every DMA whole cache lines; lane
+//        l of DMA i fetches row 8i + l / 8, chunk (l % 8) ^ (l / 8) into slot l % 8, so the 32
+//        lanes that later read one chunk of 32 rows hit distinct bank groups 8 at a time;
+//   weights: the 1 KB each row tile contributes to the block, lane l's 16 bytes at 16 l (the
+//        bytes lane l reads back): whole lines when the weight is held lane-ordered (TW, the
+//        planner's copy of a constant weight), 32 B from each of 32 rows otherwise;
+//   scale (and min) rows: the work-group's [RW][ng] rows as they lie in the tables, once.
+// Every operand arrives by DMA, so the kernel orders them with explicit vmcnt waits alone; a
+// compiler-visible load among them would get the compiler's own wait, which does not count the
+// DMAs and would wait for the next block's as well.
+template <bool SYM, int AT, int NT, int MT, bool TW>
+__global__ void __launch_bounds__(QMM_NW * 64) quant_mm_fused_k(QuantArgs a) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+  constexpr uint32_t PMASK = 0x000F000Fu;
+  constexpr uint32_t MAGIC = AT == GT_BF16 ? 0x43004300u : 0x64006400u;
+  constexpr float MAGICV = AT == GT_BF16 ? 128.f : 1024.f;
+  constexpr uint32_t CX = MAGIC | (SYM ? 0x00080008u : 0u);
+  constexpr float OFF = SYM ? 8.f : 0.f;
+  constexpr uint32_t ONES = AT == GT_BF16 ? 0x3F803F80u : 0x3C003C00u;
+  constexpr uint32_t SEL[2] = {0x05040100u, 0x07060302u};  // v_perm_b32: half p of src1 | half p of src0
+  constexpr int RW = 32 * NT, MP = 32 * MT;
+  constexpr int ABYTES = MP * 128, SBYTES = ABYTES + NT * 1024;  // one stage: act block + weight blocks
+  constexpr int NDA = ABYTES / 1024, NDS = NDA + NT;               // act DMAs, all DMAs of a stage
+  extern __shared__ __attribute__((aligned(1024))) unsigned char qmm_lds[];
+  KU_LDS unsigned char* lds = (KU_LDS unsigned char*)qmm_lds;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, h = lane >> 5;
+  const int64_t K = a.k, N = a.n, M = a.m, rb = K / 2, ng = K / a.group;
+  const int64_t n0 = (int64_t)blockIdx.x * RW;
+  // LDS: scale rows [RW][ng] f16, min rows after them (both 1 KB aligned), then two stage buffers
+  // per wave; the wave partials of the end reuse it from the start
+  const uint32_t tbl = (uint32_t)(RW * ng * 2), tblr = (tbl + 1023u) & ~1023u;
+  KU_LDS unsigned char* st0 = lds + (SYM ? tblr : 2 * tblr) + wave * 2 * SBYTES;
+  KU_LDS unsigned char* st1 = st0 + SBYTES;
+  {
+    const uint32_t nrec = (uint32_t)((N - n0 < RW ? N - n0 : RW) * ng * 2);  // rows past N read 0
+    const auto RS = qrsrc(a.scales + n0 * ng, nrec);
+    for (uint32_t i = wave; i * 1024 < tbl; i += QMM_NW) lds_dma16(RS, i * 1024 + lane * 16, 0, lds + i * 1024);
+    if constexpr (!SYM) {
+      const auto RM = qrsrc(a.mins + n0 * ng, nrec);
+      for (uint32_t i = wave; i * 1024 < tbl; i += QMM_NW)
+        lds_dma16(RM, i * 1024 + lane * 16, 0, lds + tblr + i * 1024);
+    }
+  }
+  const KU_LDS uint16_t* ssc = (const KU_LDS uint16_t*)lds;
+  const KU_LDS uint16_t* smn = (const KU_LDS uint16_t*)(lds + tblr);
+  const unsigned char* actb = static_cast<const unsigned char*>(a.act);
+  const uint32_t abytes = (uint32_t)(M * K * 2);  // act rows past M read 0
+  uint32_t aoff[NDA];
+#pragma unroll
+  for (int i = 0; i < NDA; ++i)
+    aoff[i] = (uint32_t)((8 * i + (lane >> 3)) * K * 2) + (uint32_t)(((lane & 7) ^ (lane >> 3)) << 4);
+  const int64_t ntiles = (N + 31) / 32, nblk = K / 64;
+  const uint32_t wbytes = (uint32_t)(TW ? ntiles * nblk * 1024 : N * rb);  // tiles / rows past N read 0
+  uint32_t woff[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+    woff[t] = TW ? (uint32_t)((n0 / 32 + t) * nblk * 1024 + lane * 16) : (uint32_t)((n0 + 32 * t + l32) * rb + 16 * h);
+  auto issue = [&](int blk, KU_LDS unsigned char* st) __attribute__((always_inline)) {
+    // the block offset moves the descriptors' bases: the range check does not see soffset
+    const auto RA = qrsrc(actb + blk * 128, abytes - (uint32_t)blk * 128);
+#pragma unroll
+    for (int i = 0; i < NDA; ++i) lds_dma16(RA, aoff[i], 0, st + i * 1024);
+    const uint32_t wo = TW ? (uint32_t)blk * 1024 : (uint32_t)blk * 32;
+    const auto RW_ = qrsrc(a.qw + wo, wbytes - wo);
+#pragma unroll
+    for (int t = 0; t < NT; ++t) lds_dma16(RW_, woff[t], 0, st + ABYTES + t * 1024);
+  };
+  f32x16 acc[NT][MT], cg[NT][MT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[t][mt][v] = 0.f;
+  float as[MT];
+  // block bb (0, 1) of a sub-group from a stage buffer: the act sums, then k-step jj of the MFMAs
+  // takes word 4h + jj of each row and act pairs (p, p + 4) of the same 8 values
+  auto block = [&](const KU_LDS unsigned char* st, int bb) __attribute__((always_inline)) {
+    u32x4 v[MT][4], wv[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v[mt][q] = *(const KU_LDS u32x4*)(st + (32 * mt + l32) * 128 + (((4 * h + q) ^ (l32 & 7)) << 4));
+#pragma unroll
+    for (int t = 0; t < NT; ++t) wv[t] = *(const KU_LDS u32x4*)(st + ABYTES + t * 1024 + lane * 16);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (bb == 0) as[mt] = 0.f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) as[mt] = dot2<AT>(v[mt][q][i], ONES, as[mt]);
+    }
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      u32x4 bf[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int p = 0; p < 4; ++p) bf[mt][p] = __builtin_amdgcn_perm(v[mt][jj][(p + 4) >> 1], v[mt][jj][p >> 1], SEL[p & 1]);
+#pragma unroll
+      for (int t = 0; t < NT; ++t) {
+        u32x4 af;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) af[p] = __builtin_amdgcn_bitop3_b32(wv[t][jj] >> (4 * p), CX, PMASK, 0x6c);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const f32x16 c = (bb == 0 && jj == 0) ? f32x16{} : cg[t][mt];  // the sub-group starts from zero
+          if constexpr (AT == GT_BF16)
+            cg[t][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af),
+                                                                __builtin_bit_cast(bf16x8, bf[mt]), c, 0, 0, 0);
+          else
+            cg[t][mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, af),
+                                                               __builtin_bit_cast(f16x8, bf[mt]), c, 0, 0, 0);
+        }
+      }
+    }
+  };
+  // the sub-group's fold: act sum of this lane's row over both lane halves, then the scales
+  auto fold = [&](int sg) __attribute__((always_inline)) {
+    const int g = (int)((int64_t)sg * 128 / a.group);
+    float at[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(as[mt]), __float_as_uint(as[mt]), false, false);
+      at[mt] = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = 32 * t + 8 * (v >> 2) + 4 * h + (v & 3);  // C row = weight row of the tile
+        const float sc = f16_to_f32(ssc[r * ng + g]);
+        const float mn = SYM ? 0.f : f16_to_f32(smn[r * ng + g]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          acc[t][mt][v] = fmaf(sc, fmaf(-(MAGICV + OFF), at[mt], cg[t][mt][v]), acc[t][mt][v]);
+          if constexpr (!SYM) acc[t][mt][v] = fmaf(mn, at[mt], acc[t][mt][v]);
+        }
+      }
+  };
+  // each wave a contiguous run of sub-groups; block 2 sg in st0, block 2 sg + 1 in st1
+  const int nsg = (int)(K / 128);
+  const int spw = (nsg + QMM_NW - 1) / QMM_NW, sbeg = wave * spw, send = min(nsg, sbeg + spw);
+  if (sbeg < send) {
+    issue(2 * sbeg, st0);
+    vm_wait<NDS>();  // this wave's scale-row DMAs, issued before the stage, have landed
+  } else {
+    vm_wait<0>();
+  }
+  __syncthreads();  // every wave's scale rows are in LDS
+  for (int sg = sbeg; sg < send; ++sg) {
+    issue(2 * sg + 1, st1);  // st1 was last read by the previous sub-group's second block
+    vm_wait<NDS>();          // block 2 sg is in st0
+    block(st0, 0);
+    if (sg + 1 < send) {
+      issue(2 * sg + 2, st0);
+      vm_wait<NDS>();  // block 2 sg + 1 is in st1
+    } else {
+      vm_wait<0>();
+    }
+    block(st1, 1);
+    fold(sg);
+  }
+  // partials of the waves through LDS (nothing reads the scale rows or the stages any more)
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(qmm_lds);  // [wave][t][mt][v][lane]
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) red[(((wave * NT + t) * MT + mt) * 16 + v) * 64 + lane] = acc[t][mt][v];
+  __syncthreads();
+  constexpr int PER = NT * MT * 16 * 64;  // elements of one wave's partial
+  for (int e = tid; e < PER; e += QMM_NW * 64) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < QMM_NW; ++w) sum += red[w * PER + e];
+    const int ln = e & 63, v = (e >> 6) & 15, mt = (e >> 10) % MT, t = (e >> 10) / MT;
+    const int64_t m = 32 * mt + (ln & 31);
+    const int64_t n = n0 + 32 * t + 8 * (v >> 2) + 4 * (ln >> 5) + (v & 3);
+    if (m < M && n < N) act_st<AT>(a.out, m * N + n, sum);
+  }
+}
+
+// The lane-ordered weight of the fused kernel: wt[tile][blk][lane][16 B] = the 16 bytes lane l
+// (row l % 32 of the 32-row tile, half l / 32 of the 64-value block) takes, rows past N repeating
+// row N - 1 (their results are never stored). One thread per 16 bytes.
+__global__ void __launch_bounds__(256) quant_tile_weights_k(const uint8_t* __restrict__ w, uint8_t* __restrict__ wt,
+                                                             int64_t n, int64_t k) {
+  const int64_t nblk = k / 64, ntiles = (n + 31) / 32, rb = k / 2;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (tile, blk, lane), lane fastest
+  if (i >= ntiles * nblk * 64) return;
+  const int lane = (int)(i & 63);
+  const int64_t blk = (i >> 6) % nblk, tile = (i >> 6) / nblk;
+  const int64_t row = tile * 32 + (lane & 31) < n ? tile * 32 + (lane & 31) : n - 1;
+  *reinterpret_cast<u32x4*>(wt + i * 16) = *reinterpret_cast<const u32x4*>(w + row * rb + blk * 32 + 16 * (lane >> 5));
+}
+
+// LDS bytes of the fused kernel (its stages and scale rows; the wave partials fit inside)
+static size_t quant_fused_lds(int64_t m, int64_t k, int64_t group, bool sym) {
+  const int nt = m <= 32 ? 2 : 1, mt = m <= 32 ? 1 : 2;
+  const size_t tblr = ((size_t)(32 * nt * (k / group) * 2) + 1023) & ~(size_t)1023;
+  return (sym ? 1 : 2) * tblr + (size_t)QMM_NW * 2 * (32 * mt * 128 + nt * 1024);
+}
+
+template <bool SYM, int AT, int NT, int MT>
+void launch_fused(const QuantArgs& a, hipStream_t s) {
+  const size_t lds = quant_fused_lds(a.m, a.k, a.group, SYM);
+  const dim3 grid((unsigned)((a.n + 32 * NT - 1) / (32 * NT)));
+  if (a.qw_tiled) hipLaunchKernelGGL((quant_mm_fused_k<SYM, AT, NT, MT, true>), grid, dim3(QMM_NW * 64), lds, s, a);
+  else hipLaunchKernelGGL((quant_mm_fused_k<SYM, AT, NT, MT, false>), grid, dim3(QMM_NW * 64), lds, s, a);
+}
+
 template <bool SYM, int AT, int NT, int MT>
 void launch_mm(const QuantArgs& a, hipStream_t s) {
   const int64_t ng = a.k / a.group;
@@ -641,8 +873,14 @@ void launch_mm(const QuantArgs& a, hipStream_t s) {
 
 template <bool SYM, int AT>
 void mm_at(const QuantArgs& a, hipStream_t s) {
-  if (a.m <= 32) launch_mm<SYM, AT, 2, 1>(a, s);
-  else launch_mm<SYM, AT, 1, 2>(a, s);
+  if (quant_mm_fused_ok(a)) {
+    if (a.m <= 32) launch_fused<SYM, AT, 2, 1>(a, s);
+    else launch_fused<SYM, AT, 1, 2>(a, s);
+  } else if (a.m <= 32) {
+    launch_mm<SYM, AT, 2, 1>(a, s);
+  } else {
+    launch_mm<SYM, AT, 1, 2>(a, s);
+  }
 }
 
 // one thread per packed byte of the weight: its 8/BITS values into wdq [N, K] (dtype WT)
@@ -754,7 +992,27 @@ bool quant_mm_ok(const QuantArgs& a) {
          (a.sym || a.mins);
 }
 
+bool quant_mm_fused_ok(const QuantArgs& a) {
+  if (!quant_mm_ok(a) || a.group % 128 != 0) return false;
+  // 32-bit buffer offsets and byte counts, including the rows / tiles a last work-group's lanes
+  // address past N (64 rows at most)
+  const int64_t lim = int64_t(1) << 31;
+  return quant_act_rows(a.m) * a.k * 2 < lim && (a.n + 64) * (a.k / 2) < lim && a.n * (a.k / a.group) * 2 < lim &&
+         quant_fused_lds(a.m, a.k, a.group, a.sym) <= 160 * 1024;
+}
+
+size_t quant_tiled_bytes(int64_t n, int64_t k) { return (size_t)((n + 31) / 32 * (k / 64) * 1024); }
+
+void launch_quant_tile_weights(const uint8_t* qw, uint8_t* wt, int64_t n, int64_t k, hipStream_t s) {
+  if (n <= 0 || k <= 0 || k % 64) throw std::runtime_error("quant: tiling needs n > 0 and k a multiple of 64");
+  if ((reinterpret_cast<uintptr_t>(qw) & 15) || (reinterpret_cast<uintptr_t>(wt) & 15))
+    throw std::runtime_error("quant: packed weight and its tiled copy must be 16-byte aligned");
+  const int64_t threads = (int64_t)(quant_tiled_bytes(n, k) / 16);
+  hipLaunchKernelGGL(quant_tile_weights_k, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, qw, wt, n, k);
+}
+
 size_t quant_mm_scratch_bytes(const QuantArgs& a) {
+  if (quant_mm_fused_ok(a)) return 0;  // the fused kernel stages act itself
   const int64_t nsg = a.k / (64 * (a.group % 128 == 0 ? 2 : 1));
   return quant_actp_bytes(a.m, a.k) + (size_t)(nsg * quant_act_rows(a.m) * 2) * sizeof(float);
 }
@@ -763,7 +1021,9 @@ void launch_quant_mm(const QuantArgs& a, hipStream_t s) {
   check(a);
   if (!quant_mm_ok(a)) throw std::runtime_error("quant: shape not supported by the fused MFMA kernel");
   if (a.n == 0) return;
-  if (!a.mm_scratch || (reinterpret_cast<uintptr_t>(a.mm_scratch) & 15))
+  const bool fused = quant_mm_fused_ok(a);
+  if (a.qw_tiled && !fused) throw std::runtime_error("quant: a lane-ordered weight needs the fused MFMA kernel");
+  if (!fused && (!a.mm_scratch || (reinterpret_cast<uintptr_t>(a.mm_scratch) & 15)))
     throw std::runtime_error("quant: the MFMA path needs a 16-byte aligned scratch of quant_mm_scratch_bytes()");
   if ((reinterpret_cast<uintptr_t>(a.qw) & 15) || (reinterpret_cast<uintptr_t>(a.act) & 15))
     throw std::runtime_error("quant: packed weight and act must be 16-byte aligned");

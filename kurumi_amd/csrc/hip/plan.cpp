@@ -1121,7 +1121,15 @@ void Planner::visit_quant(NodeId id) {
   Q.path = quant_gemv_ok(qa) ? QuantStep::GEMV : (quant_mm_ok(qa) ? QuantStep::MFMA : QuantStep::DEQUANT_GEMM);
   if (Q.path == QuantStep::DEQUANT_GEMM)
     Q.wdq_slot = new_slot(SlotKind::Temp, Q.wdq_dtype, Q.n * Q.k * dt_width(Q.wdq_dtype), id);
-  if (Q.path == QuantStep::MFMA) Q.mm_slot = new_slot(SlotKind::Temp, DType::U8, quant_mm_scratch_bytes(qa), id);
+  if (Q.path == QuantStep::MFMA) {
+    if (quant_mm_fused_ok(qa)) {
+      // a constant weight, whole: the fused kernel reads its lane-ordered copy
+      Q.tile_const = P_.slots_[Q.qw_slot].kind == SlotKind::Const && Q.qw_off == 0 &&
+                     P_.slots_[Q.qw_slot].bytes == Q.n * Q.k / 2;
+    } else {
+      Q.mm_slot = new_slot(SlotKind::Temp, DType::U8, quant_mm_scratch_bytes(qa), id);
+    }
+  }
   P_.quants_.push_back(Q);
   int step = new_step(Step::QUANT, (int)P_.quants_.size() - 1, "quant");
   for (int i = 0; i < 4; ++i)
@@ -1691,11 +1699,33 @@ Plan::Plan(const Graph& g, const std::vector<NodeId>& roots, Context* ctx, Const
   compile();
   if (ctx_) {
     allocate();
-    for (auto& s : slots_)
+    std::map<int, ConstEntry*> const_of;  // slot -> its cache entry
+    for (size_t i = 0; i < slots_.size(); ++i) {
+      Slot& s = slots_[i];
       if (s.kind == SlotKind::Const) {
         const_refs_.push_back(consts->get(g, s.node));
         s.buf = const_refs_.back()->buf;
         s.borrowed = true;
+        const_of[(int)i] = const_refs_.back().get();
+      }
+    }
+    for (QuantStep& Q : quants_)
+      if (Q.tile_const) {
+        ConstEntry* e = const_of.at(Q.qw_slot);
+        if (!e->tiled.ptr || e->tiled_n != (int64_t)Q.n || e->tiled_k != (int64_t)Q.k) {
+          if (e->tiled.ptr) {
+            e->nbytes -= e->tiled.bytes;
+            e->pool->release(e->tiled);
+          }
+          e->tiled = ctx_->pool().alloc(quant_tiled_bytes((int64_t)Q.n, (int64_t)Q.k));
+          e->tiled_n = (int64_t)Q.n;
+          e->tiled_k = (int64_t)Q.k;
+          e->nbytes += e->tiled.bytes;
+          launch_quant_tile_weights(static_cast<const uint8_t*>(e->buf.ptr), static_cast<uint8_t*>(e->tiled.ptr),
+                                    (int64_t)Q.n, (int64_t)Q.k, ctx_->stream());
+          KU_HIP(hipGetLastError());
+        }
+        Q.qw_tiled = e->tiled.ptr;
       }
   }
   bg_ = nullptr;
@@ -1856,7 +1886,11 @@ void Plan::launch_step(const Step& s) {
     if (Q.path == QuantStep::GEMV) {
       launch_quant_gemv(a, st);
     } else if (Q.path == QuantStep::MFMA) {
-      a.mm_scratch = slot_ptr(slots_, Q.mm_slot);
+      if (Q.mm_slot >= 0) a.mm_scratch = slot_ptr(slots_, Q.mm_slot);
+      if (Q.qw_tiled) {
+        a.qw = static_cast<const uint8_t*>(Q.qw_tiled);
+        a.qw_tiled = true;
+      }
       launch_quant_mm(a, st);
     } else {
       a.wdq = slot_ptr(slots_, Q.wdq_slot);

@@ -119,6 +119,8 @@ struct GemmStep {
 
 // Weight-only quantized matmul: a fused dequant GEMV (M <= 8), the fused dequant MFMA kernel
 // (int4, 9 <= M <= 64), else a dequantize pass into `wdq_slot` followed by a GEMM of act x wdq^T.
+// `tile_const`: the MFMA path's fused kernel reads a constant weight from its lane-ordered copy
+// (`qw_tiled`, held by the constant's cache entry).
 struct QuantStep {
   enum Path { GEMV, MFMA, DEQUANT_GEMM };
   Path path = GEMV;
@@ -128,6 +130,8 @@ struct QuantStep {
   int bits = 4;
   bool sym = true;
   DType act_dtype = DType::BF16, wdq_dtype = DType::BF16;
+  bool tile_const = false;
+  const void* qw_tiled = nullptr;
 };
 
 struct AttnStep {
@@ -158,14 +162,21 @@ struct Step {
 };
 
 // One uploaded constant. Plans hold it through a shared_ptr, so a buffer is returned to the
-// pool only once neither the cache nor any plan uses it.
+// pool only once neither the cache nor any plan uses it. A packed int4 weight that the fused
+// QuantMatmul kernel reads also gets its lane-ordered copy (`tiled`, made once, on the stream
+// right after the upload), counted in `nbytes` and freed with the entry.
 struct ConstEntry {
   Pool* pool = nullptr;
   DevBuf buf;
+  DevBuf tiled;
+  int64_t tiled_n = 0, tiled_k = 0;
   size_t nbytes = 0;
   uint64_t last_use = 0;
   ~ConstEntry() {
-    if (pool) pool->release(buf);
+    if (pool) {
+      pool->release(buf);
+      if (tiled.ptr) pool->release(tiled);
+    }
   }
 };
 

@@ -98,6 +98,38 @@ def test_quant_mfma_path_matches_oracle(hip, m, sym, act_dt, group):
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="quant mfma vs oracle")
 
 
+@pytest.mark.parametrize("m,n,k,group,sym", [(17, 100, 512, 128, True), (32, 300, 1024, 256, False),
+                                             (40, 100, 2048, 128, True), (64, 70, 512, 128, False)])
+def test_quant_mfma_weight_input_matches_constant(hip, m, n, k, group, sym):
+    """The fused MFMA kernel reads a constant weight from the planner's lane-ordered copy and a
+    weight fed as an input as it is (row-major): the same products and sums in the same order, so
+    the two are bit-identical, and both match the oracle. Rows (70, 100, 300) cut the 32-row
+    tiles; M = 40 and 64 take the 64-row act tile."""
+    print(f"quant mfma weight input m={m} n={n} k={k} g={group} sym={sym}", flush=True)
+    gc, xc, yc, xt, truth = build(m, n, k, 4, group, sym, DType.BF16, 900 + m)
+    steps = [l for l in gc.codegen([yc]).splitlines() if l.startswith("// step ")]
+    assert any("quant_mfma" in st for st in steps), steps
+    const = hip.eval_with(gc, yc, {xc: xt})
+    rng = np.random.default_rng(900 + m)
+    w = rng.standard_normal((n, k)).astype(np.float32)  # the weights build() quantised
+    p, s, mn = K.quantize(w, 4, group, sym)
+    g = Graph()
+    x = g.input([m, k], DType.BF16)
+    qw = g.input(list(p.shape), DType.U8)
+    sc = g.input(list(s.shape), DType.F16)
+    mnn = None if mn is None else g.input(list(mn.shape), DType.F16)
+    y = g.quant_matmul(x, qw, sc, mnn, 4, group)
+    feeds = {x: xt, qw: Tensor.from_numpy(p), sc: Tensor.from_numpy(s, DType.F16)}
+    if mnn is not None:
+        feeds[mnn] = Tensor.from_numpy(mn, DType.F16)
+    fed = hip.eval_with(g, y, feeds)
+    assert bytes(fed.data) == bytes(const.data), "weight input and constant weight differ"
+    got = to_f32(fed)
+    assert rel_err(got, truth) <= 1e-2, rel_err(got, truth)
+    want = to_f32(interpret(g, [y], feeds)[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="quant mfma (weight input) vs oracle")
+
+
 def test_quant_mfma_batched_decode_size(hip):
     """A batch of 32 tokens through the int4 (group 128) [11008, 4096] projection."""
     print("quant mfma 32x4096 -> 11008", flush=True)
