@@ -73,9 +73,9 @@ void launch_quant_gemv(const QuantArgs& a, hipStream_t s);
 void launch_quant_dequant(const QuantArgs& a, hipStream_t s);
 // fused dequant MFMA kernel: int4, bf16 / f16 act, 9 <= M <= 64, group a multiple of 64
 bool quant_mm_ok(const QuantArgs& a);
-// scratch of the MFMA path: act re-laid out in the order the kernel's lanes load it (whole lines
-// per load instruction) and its per-sub-group sums, written by one small pass shared by every
-// work-group
+// scratch of the MFMA path when it runs the act pass (groups not a multiple of 128): act re-laid
+// out in the order the kernel's lanes load it (whole lines per load instruction) and its
+// per-sub-group sums, written by one small pass shared by every work-group; 0 for the fused kernel
 size_t quant_mm_scratch_bytes(const QuantArgs& a);
 // whether the MFMA path runs the fused kernel (groups a multiple of 128, operands under 2 GiB),
 // which needs no scratch and can read a weight held in its lane order

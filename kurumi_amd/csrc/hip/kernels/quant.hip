@@ -10,7 +10,10 @@
 // value a thread loads, and their 16-byte chunks are all in flight at once. With bf16 / f16 act
 // and 2- or 4-bit fields the products run on v_dot2 pairs (one v_bitop3 turns two fields into a
 // 16-bit pair), which keeps the VALU work per weight byte below the HBM time.
-// quant_mm_k (int4, bf16 / f16 act, 9 <= M <= 64): the same register conversion feeds the MFMAs.
+// quant_mm_fused_k (int4, bf16 / f16 act, 9 <= M <= 64, groups a multiple of 128): the same
+// register conversion feeds the MFMAs, both operands staged through LDS by whole-line DMA (a
+// constant weight from its lane-ordered copy); quant_mm_k, after the act pass quant_act_prep_k,
+// for the other groups.
 // quant_dequant_k (everything else): the weight is expanded once into act's dtype (f32, bf16 or
 // f16) for the MFMA / generic GEMM; bf16 / f16 round each dequantized weight once, the f32
 // products then accumulate in f32 like the reference.
