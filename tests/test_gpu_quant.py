@@ -130,6 +130,46 @@ def test_quant_mfma_weight_input_matches_constant(hip, m, n, k, group, sym):
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="quant mfma (weight input) vs oracle")
 
 
+def test_quant_constant_weight_shared_by_plans(hip):
+    """One constant int4 weight in several plans on one backend: the batched path's plans (M = 32
+    and M = 17) read the lane-ordered copy the constant's cache entry holds, made by the first of
+    them; the decode plan (M = 1) reads the packed bytes themselves. Dropping the plan that made
+    the copy leaves it to the others (it lives as long as the constant), so every plan, launched
+    again afterwards, still matches the oracle."""
+    import gc
+    n, k, group = 300, 1024, 128
+    rng = np.random.default_rng(41)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    p, s, _ = K.quantize(w, 4, group, True)
+    plans = {}
+    for m in (32, 17, 1):
+        g = Graph()
+        x = g.input([m, k], DType.BF16)
+        qw = g.constant_bytes(DType.U8, p.tobytes(), p.shape)
+        sc = g.constant_bytes(DType.F16, s.tobytes(), s.shape)
+        y = g.quant_matmul(x, qw, sc, None, 4, group)
+        act = rng.standard_normal((m, k)).astype(np.float32)
+        xt = interpret(*(lambda gg: (gg, [gg.cast(gg.constant(act), DType.BF16)]))(Graph()))[0]
+        plan = hip.plan(g, [y], {x: xt})
+        assert plan.steps()[0].startswith("quant_mfma" if m > 8 else "quant_gemv"), plan.steps()
+        plans[m] = (plan, g, x, y, xt)
+
+    def check(m):
+        plan, g, x, y, xt = plans[m]
+        plan.launch()
+        plan.sync()
+        got = to_f32(plan.output(0))
+        want = to_f32(interpret(g, [y], {x: xt})[0])
+        assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what=f"shared weight m={m}")
+
+    for m in (32, 17, 1):
+        check(m)
+    del plans[32]  # the plan whose build made the lane-ordered copy
+    gc.collect()
+    for m in (17, 1):
+        check(m)
+
+
 def test_quant_mfma_batched_decode_size(hip):
     """A batch of 32 tokens through the int4 (group 128) [11008, 4096] projection."""
     print("quant mfma 32x4096 -> 11008", flush=True)
