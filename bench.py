@@ -255,7 +255,7 @@ def bench_cfg2(hip, steps, warmup, dt_name="f32"):
         gw, gper, _ = time_plans([c.plan], steps, warmup, use_graph=True, warm_ms=0.0)
         out["graph_replay"] = {"ms_per_step": gw, "kernel_ms": gper[0],
                                "gbs": c.algo_bytes / (gper[0] * 1e-3) / 1e9}
-        out["_cfg"] = c
+    out["_cfg"] = c
     return out
 
 
@@ -407,40 +407,58 @@ def _oracle():
     return kutest
 
 
-def _time_cpu(fn, budget_s, max_reps=20):
-    fn()  # warm-up
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        fn()
-        reps += 1
-        el = time.perf_counter() - t0
-        if el > budget_s or reps >= max_reps:
-            return el / reps, reps
+def _time_cpu(run, budget_s, max_reps=20):
+    """Average seconds of `run()` (the oracle call alone: it returns raw output handles, released
+    outside the timed span) with this thread pinned to one core, so the figure is single-core
+    whatever threads the call starts (they inherit the affinity). The affinity is restored after."""
+    kt = _oracle()
+    saved = os.sched_getaffinity(0)
+    os.sched_setaffinity(0, {min(saved)})
+    try:
+        kt.free_raw(run())  # warm-up
+        reps, total = 0, 0.0
+        while True:
+            t0 = time.perf_counter()
+            out = run()
+            total += time.perf_counter() - t0
+            kt.free_raw(out)
+            reps += 1
+            if total > budget_s or reps >= max_reps:
+                return total / reps, reps
+    finally:
+        os.sched_setaffinity(0, saved)
 
 
 def _cpu_line(value, unit, sample, reps, sec):
     return {"value": value, "unit": unit, "cores": 1, "kind": "port",
-            "sample": f"{sample}; {reps} reps, {sec * 1e3:.1f} ms/rep; host nproc={os.cpu_count()}"}
+            "sample": f"{sample}; {reps} reps, {sec * 1e3:.1f} ms/rep; pinned to one core of host "
+                      f"nproc={os.cpu_count()}; inputs bound and outputs released outside the timed call"}
 
 
-def cpu_baseline_cfg2(xt_full, rows_sample=1024, cols=32000):
+def cpu_baseline_cfg2(xt_full, dt_name="f32", rows_sample=None, cols=32000):
     """The oracle interpreter on a row sample of the same logits (rows are independent), about
-    10 s of single-core work."""
+    10 s of single-core work: f32 through the decomposed primitives, bf16 through the same chain
+    with the interpreter's per-primitive bf16 rounding (interp/elementwise.rs, interp/nn.rs:18-33)."""
     kt, K = _oracle(), _ku()
+    bf16 = dt_name == "bf16"
+    rows_sample = rows_sample or (256 if bf16 else 1024)
+    dt = K.DType.BF16 if bf16 else K.DType.F32
     xs = np.ascontiguousarray(xt_full.numpy()[:rows_sample])
-    g, x, y, a = softmax_graph(K, rows_sample, cols, K.DType.F32)
-    feeds = {x: K.Tensor.from_numpy(xs)}
-    sec, reps = _time_cpu(lambda: kt.interpret(g, [y, a], feeds), 10.0)
-    algo_bytes = rows_sample * cols * 8 + rows_sample * 4
+    g, x, y, a = softmax_graph(K, rows_sample, cols, dt)
+    f = K.Feeds({x: K.Tensor(dt, [rows_sample, cols], xs.tobytes())})
+    sec, reps = _time_cpu(lambda: kt.interpret_raw(g, [y, a], f), 10.0)
+    w = 2 if bf16 else 4
+    algo_bytes = rows_sample * cols * 2 * w + rows_sample * 4
     return _cpu_line(round(algo_bytes / sec / 1e9, 4), "GB/s",
-                     f"{rows_sample} of 8192 rows x 32000 f32, decomposed softmax + argmax via the oracle "
+                     f"{rows_sample} of 8192 rows x 32000 {dt_name}, decomposed softmax + argmax via the oracle "
                      f"interpreter", reps, sec)
 
 
 def cpu_baseline_cfg1(c):
     """The view-fused CPU path (restated realize::force) on the full cfg 1 input."""
-    kt = _oracle()
-    sec, reps = _time_cpu(lambda: kt.realize(c.g, c.roots[0], c.feeds), 4.0)
+    kt, K = _oracle(), _ku()
+    f = K.Feeds(c.feeds)
+    sec, reps = _time_cpu(lambda: kt.realize_raw(c.g, c.roots[0], f), 4.0)
     return _cpu_line(round(c.algo_bytes / sec / 1e9, 4), "GB/s",
                      "full [4096,4096] f32 through the view-fused realize path", reps, sec)
 
@@ -464,7 +482,8 @@ def cpu_baseline_gemm(c, batched):
         src_b = c.feeds[c.b].numpy()
     feeds = {a: K.Tensor(K.DType.BF16, sa, np.ascontiguousarray(src_a).tobytes()),
              b: K.Tensor(K.DType.BF16, sb, np.ascontiguousarray(src_b).tobytes())}
-    sec, reps = _time_cpu(lambda: kt.interpret(g, [y], feeds), 4.0, 5)
+    f = K.Feeds(feeds)
+    sec, reps = _time_cpu(lambda: kt.interpret_raw(g, [y], f), 4.0, 5)
     flops = 2 * int(np.prod(sa)) * sb[-1]
     return _cpu_line(round(flops / sec / 1e9, 4), "GFLOP/s",
                      f"{sa}@{sb} bf16 (sub-shape of the config) via the oracle interpreter", reps, sec)
@@ -479,7 +498,8 @@ def cpu_baseline_attention(c):
     o = g.sdpa_fused(q, k, v, True)
     feeds = {n: K.Tensor(K.DType.BF16, [1, 1, S, D], np.ascontiguousarray(c.feeds[src].numpy()[:1, :1]).tobytes())
              for n, src in ((q, c.q), (k, c.k), (v, c.v))}
-    sec, reps = _time_cpu(lambda: kt.interpret(g, [o], feeds), 4.0, 3)
+    f = K.Feeds(feeds)
+    sec, reps = _time_cpu(lambda: kt.interpret_raw(g, [o], f), 4.0, 3)
     flops = 4 * S * S * D // 2
     return _cpu_line(round(flops / sec / 1e9, 4), "GFLOP/s",
                      "one (batch, head) slice [1,1,2048,128] bf16 causal via the oracle interpreter", reps, sec)
@@ -490,7 +510,8 @@ def cpu_baseline_fp8(c, rows=8):
     kt, K = _oracle(), _ku()
     g, x, y = fp8_graph(K, [rows, c.K], c.w.data, [c.N, c.K])
     feeds = {x: K.Tensor(K.DType.BF16, [rows, c.K], np.ascontiguousarray(c.feeds[c.x].numpy()[:rows]).tobytes())}
-    sec, reps = _time_cpu(lambda: kt.interpret(g, [y], feeds), 4.0, 5)
+    f = K.Feeds(feeds)
+    sec, reps = _time_cpu(lambda: kt.interpret_raw(g, [y], f), 4.0, 5)
     flops = 2 * rows * c.N * c.K
     return _cpu_line(round(flops / sec / 1e9, 4), "GFLOP/s",
                      f"[{rows},{c.K}] x [{c.N},{c.K}]^T e4m3 linear (sub-shape) via the oracle interpreter", reps, sec)
@@ -547,7 +568,8 @@ def main() -> int:
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_cfg2(xt)
-        for key, fn in (("cfg1", lambda c: cpu_baseline_cfg1(c)), ("cfg3", lambda c: cpu_baseline_gemm(c, False)),
+        for key, fn in (("cfg2_bf16", lambda c: cpu_baseline_cfg2(c.feeds[c.x], "bf16")),
+                        ("cfg1", lambda c: cpu_baseline_cfg1(c)), ("cfg3", lambda c: cpu_baseline_gemm(c, False)),
                         ("cfg3b", lambda c: cpu_baseline_gemm(c, True)), ("cfg4", cpu_baseline_attention),
                         ("cfg5", cpu_baseline_fp8)):
             if key in extra:

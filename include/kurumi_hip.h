@@ -239,11 +239,13 @@ KuNode ku_amp(KuGraph *g, KuNode root);
 KuNode ku_amp_fp8(KuGraph *g, KuNode root);
 
 /* ku_plan_compile on a caller's backend, sharing its plan and constant caches; run and free
- * with ku_plan_run / ku_plan_free. */
+ * with ku_plan_run / ku_plan_free. The plan keeps the backend alive: ku_backend_free may come
+ * before ku_plan_free, and the backend's device memory is released with its last plan. */
 KuPlan *ku_hip_plan_compile_on(const KuBackend *b, const KuGraph *g, KuNode node);
 
 /* Device-resident plan: compile `roots`, upload `feeds` once, then launch repeatedly with
- * inputs and outputs staying in HBM. The graph must outlive the plan. */
+ * inputs and outputs staying in HBM. The graph must outlive the plan; the backend need not (the
+ * plan keeps it alive, as ku_hip_plan_compile_on's plans do). */
 KuHipPlan *ku_hip_plan_new(KuGraph *g, const KuNode *roots, size_t n, const KuBackend *backend,
                            const KuFeeds *feeds);
 int32_t ku_hip_plan_feed(KuHipPlan *p, KuNode input, const KuTensor *t);
@@ -269,7 +271,8 @@ size_t ku_hip_codegen(KuGraph *g, const KuNode *roots, size_t n, uint32_t compil
 
 /* The e4m3 linear layer on caller-owned device buffers, the graph ku_amp_fp8 emits for one
  * layer as one call: sx = max|x| / 448 (computed on the device), xq = e4m3(x / sx) and
- * y = (xq @ wq^T) * sx * sw[n] rounded to y_dtype, on the fp8 MFMA GEMM.
+ * y = (xq @ wq^T) * sx * sw[n] rounded to y_dtype, on the fp8 MFMA GEMM. An all-zero x
+ * (sx = 0) is divided by 1 instead, so y = 0 (not NaN).
  *   x  [m, k] KU_BF16 / KU_F16 / KU_F32, wq [n, k] KU_F8E4M3 (e.g. rows quantised with per-row
  *   absmax / 448 scales sw [n] f32), y [m, n] KU_BF16 / KU_F16 / KU_F32; all row-major, 16-byte
  *   aligned device pointers; k a multiple of 128.
@@ -294,6 +297,63 @@ int32_t ku_hip_linear_e4m3_noalloc(const void *x, uint32_t x_dtype, const uint8_
  * are cached by graph content, so an equal graph rebuilt per call adds to neither); returns
  * the number of evals. */
 uint64_t ku_hip_profile(const KuBackend *b, uint64_t *out_launches, size_t cap);
+
+/* ---- collision-free entry set ----
+ *
+ * No counterpart in the reference. kurumi's own library (rlib, cdylib and staticlib of the
+ * `kurumi` crate, kurumi/Cargo.toml:12-13) exports the same unprefixed ku_* names as this one,
+ * so a process holding both (kurumi's CPU backend and C ABI plus this HIP backend) cannot reach
+ * this library through those names: the dynamic linker binds each name to whichever definition
+ * it finds first. ku_hip_api is the one name such a process binds; the table it returns points
+ * at this library's own definitions, and the library binds its internal calls to itself
+ * (linked with -Bsymbolic-functions), so every call through the table stays in
+ * libkurumi_hip.so whatever else the process exports. The table covers the backend seam: errors,
+ * backends, graphs, KGPH v2 decode, eval, plans, feeds, tensors and inspection; graphs are built
+ * with kurumi's builders and handed over as KGPH v2 bytes.
+ *
+ * ku_hip_api(KU_HIP_API_VERSION) returns the table, or NULL (and ku_last_error) for a version
+ * this library does not provide. Fields are only ever appended; `size` is sizeof the table the
+ * library was built with. */
+#define KU_HIP_API_VERSION 1u
+
+typedef struct KuHipApi {
+  uint32_t version; /* KU_HIP_API_VERSION */
+  uint32_t size;    /* sizeof(KuHipApi) */
+  const char *(*last_error)(void);
+  KuBackend *(*backend_new)(uint32_t kind);
+  void (*backend_free)(KuBackend *b);
+  KuGraph *(*graph_new)(void);
+  void (*graph_free)(KuGraph *g);
+  KuRunnable *(*graph_deserialize)(const uint8_t *bytes, size_t len);
+  KuGraph *(*runnable_take_graph)(KuRunnable *h);
+  size_t (*runnable_output_count)(const KuRunnable *h);
+  KuNode (*runnable_output)(const KuRunnable *h, size_t i);
+  size_t (*runnable_input_count)(const KuRunnable *h);
+  KuNode (*runnable_input_node)(const KuRunnable *h, size_t i);
+  size_t (*runnable_input_name)(const KuRunnable *h, size_t i, uint8_t *out, size_t cap);
+  void (*runnable_free)(KuRunnable *h);
+  KuTensor *(*eval)(KuGraph *g, KuNode node, const KuBackend *backend);
+  KuTensor *(*eval_with)(KuGraph *g, KuNode node, const KuBackend *backend, const KuFeeds *feeds);
+  int32_t (*eval_many)(KuGraph *g, const KuNode *ids, size_t n, const KuBackend *backend, const KuFeeds *feeds,
+                       KuTensor **out);
+  KuPlan *(*plan_compile_on)(const KuBackend *b, const KuGraph *g, KuNode node);
+  KuTensor *(*plan_run)(const KuPlan *p, const KuGraph *g, const KuFeeds *feeds);
+  void (*plan_free)(KuPlan *p);
+  KuFeeds *(*feeds_new)(void);
+  void (*feeds_free)(KuFeeds *f);
+  void (*feeds_set)(KuFeeds *f, KuNode node, const KuTensor *tensor);
+  KuTensor *(*tensor_new)(uint32_t dtype, const uint8_t *data, size_t nbytes, const size_t *shape, size_t rank);
+  void (*tensor_free)(KuTensor *t);
+  size_t (*tensor_rank)(const KuTensor *t);
+  void (*tensor_shape)(const KuTensor *t, size_t *out);
+  uint32_t (*tensor_dtype)(const KuTensor *t);
+  size_t (*tensor_nbytes)(const KuTensor *t);
+  void (*tensor_bytes)(const KuTensor *t, uint8_t *out);
+  size_t (*node_count)(const KuGraph *g, KuNode root);
+  size_t (*dump)(const KuGraph *g, KuNode root, uint8_t *out, size_t cap);
+} KuHipApi;
+
+const KuHipApi *ku_hip_api(uint32_t version);
 
 #ifdef __cplusplus
 }

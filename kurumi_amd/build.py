@@ -36,18 +36,35 @@ def sources() -> tuple[list[Path], list[Path]]:
     return host, dev
 
 
-def build(verbose: bool = False, jobs: int | None = None) -> Path:
+def _up_to_date(o: Path) -> bool:
+    """True when `o` and its dependency file exist and no listed dependency is newer."""
+    d = o.with_suffix(".d")
+    if not o.exists() or not d.exists():
+        return False
+    deps = d.read_text().replace("\\\n", " ").split(":", 1)[-1].split()
+    t = o.stat().st_mtime
+    try:
+        return all(Path(p).stat().st_mtime <= t for p in deps)
+    except FileNotFoundError:
+        return False
+
+
+def build(verbose: bool = False, jobs: int | None = None, incremental: bool = False) -> Path:
+    """Compile every source (or, with `incremental`, those whose dependencies changed) and link."""
     BUILD.mkdir(exist_ok=True)
     host, dev = sources()
     cmds = []
     objs = []
     for s in host:
         o = BUILD / (s.parent.name + "_" + s.stem + ".o")
-        cmds.append(["g++", *HOST_FLAGS, "-c", str(s), "-o", str(o)])
+        if not (incremental and _up_to_date(o)):
+            cmds.append(["g++", *HOST_FLAGS, "-MMD", "-MF", str(o.with_suffix(".d")), "-c", str(s), "-o", str(o)])
         objs.append(o)
     for s in dev:
         o = BUILD / ("k_" + s.stem + ".o")
-        cmds.append([f"{ROCM}/bin/hipcc", *HIP_FLAGS, "-c", str(s), "-o", str(o)])
+        if not (incremental and _up_to_date(o)):
+            cmds.append([f"{ROCM}/bin/hipcc", *HIP_FLAGS, "-MMD", "-MF", str(o.with_suffix(".d")), "-c", str(s), "-o",
+                         str(o)])
         objs.append(o)
     jobs = jobs or min(8, os.cpu_count() or 4)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
@@ -56,7 +73,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")
     _run([f"{ROCM}/bin/hipcc", "--offload-arch=gfx950", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs),
-          f"-L{ROCM}/lib", "-lhiprtc", "-lamdhip64", "-pthread", f"-Wl,-rpath,{ROCM}/lib"])
+          f"-L{ROCM}/lib", "-lhiprtc", "-lamdhip64", "-pthread", f"-Wl,-rpath,{ROCM}/lib",
+          # calls and function addresses inside the library bind to its own definitions, so a
+          # process that also loads kurumi's library (same ku_* names) cannot divert them
+          "-Wl,-Bsymbolic-functions"])
     os.replace(tmp, LIB)
     if verbose:
         print(f"built {LIB}")
@@ -64,5 +84,5 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, incremental="--incremental" in sys.argv)
     sys.exit(0)

@@ -22,14 +22,22 @@
 using ku::NodeId;
 using ku::Shape;
 
-struct KuBackend { std::unique_ptr<ku::hipbk::HipBackend> b; };
+// Plans keep the backend they were built on alive (shared ownership): a plan's steps use the
+// backend's stream, pools and constant cache, so freeing the KuBackend handle first only drops
+// the handle's reference and the backend ends with its last plan.
+struct KuBackend { std::shared_ptr<ku::hipbk::HipBackend> b; };
 struct KuPlan {
-  std::shared_ptr<ku::hipbk::Plan> p;
+  std::shared_ptr<ku::hipbk::HipBackend> owner;  // null for the process-default backend
+  std::shared_ptr<ku::hipbk::Plan> p;            // declared after owner: destroyed first
   uint64_t gid;              // the graph it was compiled on
   ku::hipbk::Hash128 fp;     // and that graph's content, for a run on an equal graph
   NodeId node;
 };
-struct KuHipPlan { std::unique_ptr<ku::hipbk::Plan> p; ku::hipbk::HipBackend* b; };
+struct KuHipPlan {
+  std::shared_ptr<ku::hipbk::HipBackend> owner;
+  std::unique_ptr<ku::hipbk::Plan> p;  // declared after owner: destroyed first
+  ku::hipbk::HipBackend* b;
+};
 
 namespace {
 thread_local std::string g_last_error;
@@ -77,8 +85,10 @@ ku::hipbk::HipBackend* default_backend() {
   return g_default;
 }
 
-KuPlan* compile_plan(ku::hipbk::HipBackend* b, const ku::Graph& g, KuNode node) {
+KuPlan* compile_plan(ku::hipbk::HipBackend* b, std::shared_ptr<ku::hipbk::HipBackend> owner, const ku::Graph& g,
+                     KuNode node) {
   auto* p = new KuPlan();
+  p->owner = std::move(owner);
   try {
     p->p = b->plan_for(g, {node});
     p->gid = g.id();
@@ -332,7 +342,7 @@ KuBackend* ku_backend_new(uint32_t kind) {
   return guard<KuBackend*>(nullptr, [&] {
     auto* b = new KuBackend();
     try {
-      b->b = std::make_unique<ku::hipbk::HipBackend>(0);
+      b->b = std::make_shared<ku::hipbk::HipBackend>(0);
     } catch (...) {
       delete b;
       throw;
@@ -425,14 +435,14 @@ KuPlan* ku_plan_compile(const KuGraph* g, KuNode node) {
     set_err("ku_plan_compile: null graph handle");
     return nullptr;
   }
-  return guard<KuPlan*>(nullptr, [&] { return compile_plan(default_backend(), g->g, node); });
+  return guard<KuPlan*>(nullptr, [&] { return compile_plan(default_backend(), nullptr, g->g, node); });
 }
 KuPlan* ku_hip_plan_compile_on(const KuBackend* b, const KuGraph* g, KuNode node) {
   if (!b || !g) {
     set_err("ku_hip_plan_compile_on: null backend/graph handle");
     return nullptr;
   }
-  return guard<KuPlan*>(nullptr, [&] { return compile_plan(b->b.get(), g->g, node); });
+  return guard<KuPlan*>(nullptr, [&] { return compile_plan(b->b.get(), b->b, g->g, node); });
 }
 KuTensor* ku_plan_run(const KuPlan* p, const KuGraph* g, const KuFeeds* feeds) {
   if (!p || !g || !feeds) {
@@ -526,6 +536,7 @@ KuHipPlan* ku_hip_plan_new(KuGraph* g, const KuNode* roots, size_t n, const KuBa
   }
   return guard<KuHipPlan*>(nullptr, [&] {
     auto* p = new KuHipPlan();
+    p->owner = backend->b;
     p->b = backend->b.get();
     try {
       p->p = p->b->new_plan(g->g, std::vector<NodeId>(roots, roots + n));

@@ -2,7 +2,8 @@
 //
 //   amax = max_i |x_i|   (maxNum fold from -inf, so NaNs never win: f32::max of the reference
 //                          interpreter, kurumi_core/src/dtype/traits/float.rs:36)
-//   sx   = amax * f32(1/448),  inv = 1 / sx  (IEEE division, as Op::Recip)
+//   sx   = amax * f32(1/448),  inv = 1 / sx  (IEEE division, as Op::Recip; inv = 1 unless
+//                                              sx > 0, so an all-zero x gives xq = 0 and y = 0)
 //   xq   = e4m3(f32(x) * inv)                 (round to nearest even, saturating to +-448)
 //   y    = round_out((xq @ wq^T) * sx * sw[n]) (the fp8 MFMA GEMM, scales in its epilogue)
 //
@@ -144,7 +145,8 @@ __device__ __forceinline__ void store_e4m3(uint8_t* p, const float* v, float inv
     *reinterpret_cast<uint32_t*>(p) = q[0];
 }
 
-// pass 2: fold the partials, then xq = e4m3(x * (1 / (amax * (1/448)))); work-group 0 stores sx.
+// pass 2: fold the partials, then xq = e4m3(x * (1 / (amax * (1/448)))) (1 / 1 when amax is 0);
+// work-group 0 stores sx.
 // The first trip's loads of x are issued before the partials are folded.
 template <int XT>
 __global__ __launch_bounds__(kThreads) void actq_quantise_k(const void* __restrict__ x, int64_t n,
@@ -163,7 +165,7 @@ __global__ __launch_bounds__(kThreads) void actq_quantise_k(const void* __restri
   for (int i = threadIdx.x; i < nparts; i += kThreads) m = fmaxf(m, partials[i]);
   const float amax = block_max(m, lds);
   const float sx = amax * kInv448;
-  const float inv = 1.0f / sx;
+  const float inv = 1.0f / (sx > 0.f ? sx : 1.f);  // where(0 < sx, sx, 1) of the e4m3 pass
   if (blockIdx.x == 0 && threadIdx.x == 0) sx_out[0] = sx;
   while (base < nv) {
 #pragma unroll

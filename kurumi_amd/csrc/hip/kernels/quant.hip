@@ -672,7 +672,11 @@ __global__ void __launch_bounds__(QMM_NW * 64) quant_mm_fused_k(QuantArgs a) {
   KU_LDS unsigned char* st0 = lds + (SYM ? tblr : 2 * tblr) + wave * 2 * SBYTES;
   KU_LDS unsigned char* st1 = st0 + SBYTES;
   {
-    const uint32_t nrec = (uint32_t)((N - n0 < RW ? N - n0 : RW) * ng * 2);  // rows past N read 0
+    // rows past N read 0. The byte count is rounded up to whole dwords: with an odd row count
+    // and an odd ng the table's last f16 shares a dword with the next row's first, and a range
+    // check made per dword would drop it. The rounding reads at most 2 bytes past the table, in
+    // the same pool buffer (16-byte aligned operands, buffers whole multiples of 256 bytes).
+    const uint32_t nrec = (uint32_t)(((N - n0 < RW ? N - n0 : RW) * ng * 2 + 3) & ~int64_t(3));
     const auto RS = qrsrc(a.scales + n0 * ng, nrec);
     for (uint32_t i = wave; i * 1024 < tbl; i += QMM_NW) lds_dma16(RS, i * 1024 + lane * 16, 0, lds + i * 1024);
     if constexpr (!SYM) {

@@ -1226,19 +1226,29 @@ bool Planner::match_attention(NodeId d2) {
   if (mul->op.kind == OpKind::Add) {
     // one operand is the causal bias
     NodeId x0 = mul->src[0], b0 = mul->src[1];
+    // The causal bias is Expand(Reshape(C[S,S], [1,..,1,S,S]), score shape), optionally cast
+    // (attention.rs:139-153). Both targets are checked: a 0/-inf constant reshaped to, say,
+    // [1,S,1,S] would mask along (head, key) instead of (query, key) and must stay unmatched.
+    const Shape& score_shape = g_.shape(sc);
     auto is_bias = [&](NodeId b, std::vector<NodeId>& chain) {
       NodeId cur = b;
       if (g_.node(cur).op.kind == OpKind::Cast) { if (!single(cur)) return false; chain.push_back(cur); cur = g_.node(cur).src[0]; }
       if (g_.node(cur).op.kind != OpKind::Expand || !single(cur)) return false;
+      if (g_.shape(cur) != score_shape) return false;
       chain.push_back(cur);
       cur = g_.node(cur).src[0];
       if (g_.node(cur).op.kind != OpKind::Reshape || !single(cur)) return false;
+      const Shape& rs = g_.shape(cur);
       chain.push_back(cur);
       cur = g_.node(cur).src[0];
       const Node& c = g_.node(cur);
       if (c.op.kind != OpKind::Const || c.op.data_dtype != DType::F32 || c.shape.size() != 2 || c.shape[0] != c.shape[1])
         return false;
       size_t S = c.shape[0];
+      if (rs.size() != r || rs[r - 2] != S || rs[r - 1] != S) return false;
+      for (size_t i = 0; i + 2 < r; ++i)
+        if (rs[i] != 1) return false;
+      if (score_shape[r - 2] != S || score_shape[r - 1] != S) return false;
       const float* d = reinterpret_cast<const float*>(c.op.data->data());
       for (size_t i = 0; i < S; ++i)
         for (size_t j = 0; j < S; ++j) {
@@ -1376,8 +1386,9 @@ bool Planner::match_fp8_epilogue(NodeId castn) {
 
 // The activation half of the e4m3 linear (the chain the e4m3 pass emits, ir/pass_fp8.cpp):
 //   xa = max(xf, neg(xf)), am = reduce_max(reduce_max(xa, 1), 0), sx = am * (1/448),
-//   xq = cast_e4m3(xf2 * expand(reshape(recip(sx), [1, 1]), [M, K]))
-// with xf, xf2 = x or cast_f32(x) and x a bf16 / f16 / f32 [M, K] value. It becomes one ACTQ step
+//   xq = cast_e4m3(xf2 * expand(reshape(recip(where(cmp_lt(0, sx), sx, 1)), [1, 1]), [M, K]))
+// with xf, xf2 = x or cast_f32(x) and x a bf16 / f16 / f32 [M, K] value (the where makes an
+// all-zero x divide by 1; a plain recip(sx) is accepted too). It becomes one ACTQ step
 // (two kernels) producing xq and sx, in place of three generated kernels. Every absorbed node
 // must be used only inside the chain (sx and xq may have other users: they are materialised).
 bool Planner::match_actq(NodeId xq, NodeId sx) {
@@ -1388,6 +1399,25 @@ bool Planner::match_actq(NodeId xq, NodeId sx) {
   if (kind(mul) != OpKind::Mul) return false;
   // one operand is the broadcast reciprocal of sx, the other x as f32
   NodeId inv = 0, invr = 0, invb = 0, xf2 = 0;
+  std::vector<NodeId> guard;  // the where(cmp_lt(0, sx), sx, 1) nodes, when present
+  // s = expand(const v) with every element v (the builders' scalar)
+  auto is_scalar = [&](NodeId e, double v) {
+    NodeId c = kind(e) == OpKind::Expand ? g_.node(e).src[0] : e;
+    double got;
+    return const_uniform_value(g_.node(c), &got) && got == v;
+  };
+  auto guarded = [&](NodeId w) {
+    const Node& wn = g_.node(w);
+    if (wn.op.kind != OpKind::Where || wn.src[1] != sx || !is_scalar(wn.src[2], 1.0)) return false;
+    const Node& cn = g_.node(wn.src[0]);
+    if (cn.op.kind != OpKind::CmpLt || cn.src[1] != sx || !is_scalar(cn.src[0], 0.0)) return false;
+    guard = {w, wn.src[0]};
+    for (NodeId e : {wn.src[2], cn.src[0]}) {
+      guard.push_back(e);
+      if (kind(e) == OpKind::Expand) guard.push_back(g_.node(e).src[0]);
+    }
+    return true;
+  };
   bool found = false;
   for (int t = 0; t < 2 && !found; ++t) {
     const NodeId e = g_.node(mul).src[t];
@@ -1395,7 +1425,9 @@ bool Planner::match_actq(NodeId xq, NodeId sx) {
     const NodeId r = g_.node(e).src[0];
     if (kind(r) != OpKind::Reshape || g_.shape(r) != Shape{1, 1}) continue;
     const NodeId i = g_.node(r).src[0];
-    if (kind(i) != OpKind::Recip || g_.node(i).src[0] != sx) continue;
+    if (kind(i) != OpKind::Recip) continue;
+    guard.clear();
+    if (g_.node(i).src[0] != sx && !guarded(g_.node(i).src[0])) continue;
     inv = i; invr = r; invb = e; xf2 = g_.node(mul).src[1 - t];
     found = true;
   }
@@ -1450,6 +1482,7 @@ bool Planner::match_actq(NodeId xq, NodeId sx) {
   if (!found) return false;
   // every absorbed node is used only by nodes of the chain
   std::set<NodeId> chain = {xa, ng, rm, am, inv, invr, invb, mul, sc, xq, sx};
+  chain.insert(guard.begin(), guard.end());
   if (xf != x) chain.insert(xf);
   if (xf2 != x) chain.insert(xf2);
   if (kind(sc) == OpKind::Expand) chain.insert(g_.node(sc).src[0]);
@@ -1712,20 +1745,17 @@ Plan::Plan(const Graph& g, const std::vector<NodeId>& roots, Context* ctx, Const
     for (QuantStep& Q : quants_)
       if (Q.tile_const) {
         ConstEntry* e = const_of.at(Q.qw_slot);
-        if (!e->tiled.ptr || e->tiled_n != (int64_t)Q.n || e->tiled_k != (int64_t)Q.k) {
-          if (e->tiled.ptr) {
-            e->nbytes -= e->tiled.bytes;
-            e->pool->release(e->tiled);
-          }
-          e->tiled = ctx_->pool().alloc(quant_tiled_bytes((int64_t)Q.n, (int64_t)Q.k));
-          e->tiled_n = (int64_t)Q.n;
-          e->tiled_k = (int64_t)Q.k;
-          e->nbytes += e->tiled.bytes;
-          launch_quant_tile_weights(static_cast<const uint8_t*>(e->buf.ptr), static_cast<uint8_t*>(e->tiled.ptr),
-                                    (int64_t)Q.n, (int64_t)Q.k, ctx_->stream());
+        const auto key = std::make_pair((int64_t)Q.n, (int64_t)Q.k);
+        auto it = e->tiled.find(key);
+        if (it == e->tiled.end()) {
+          DevBuf t = ctx_->pool().alloc(quant_tiled_bytes(key.first, key.second));
+          it = e->tiled.emplace(key, t).first;
+          e->nbytes += t.bytes;
+          launch_quant_tile_weights(static_cast<const uint8_t*>(e->buf.ptr), static_cast<uint8_t*>(t.ptr), key.first,
+                                    key.second, ctx_->stream());
           KU_HIP(hipGetLastError());
         }
-        Q.qw_tiled = e->tiled.ptr;
+        Q.qw_tiled = it->second.ptr;
       }
   }
   bg_ = nullptr;

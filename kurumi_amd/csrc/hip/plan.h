@@ -163,19 +163,20 @@ struct Step {
 
 // One uploaded constant. Plans hold it through a shared_ptr, so a buffer is returned to the
 // pool only once neither the cache nor any plan uses it. A packed int4 weight that the fused
-// QuantMatmul kernel reads also gets its lane-ordered copy (`tiled`, made once, on the stream
-// right after the upload), counted in `nbytes` and freed with the entry.
+// QuantMatmul kernel reads also gets a lane-ordered copy per [n, k] it is read as (one packed
+// constant may be reshaped to several; each copy is made once, on the stream, when the first
+// plan needs it), counted in `nbytes` and freed only with the entry, since plans and captured
+// hipGraphs hold its address.
 struct ConstEntry {
   Pool* pool = nullptr;
   DevBuf buf;
-  DevBuf tiled;
-  int64_t tiled_n = 0, tiled_k = 0;
+  std::map<std::pair<int64_t, int64_t>, DevBuf> tiled;  // (n, k) -> lane-ordered copy
   size_t nbytes = 0;
   uint64_t last_use = 0;
   ~ConstEntry() {
     if (pool) {
       pool->release(buf);
-      if (tiled.ptr) pool->release(tiled);
+      for (auto& kv : tiled) pool->release(kv.second);
     }
   }
 };

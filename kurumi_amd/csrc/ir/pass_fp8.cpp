@@ -6,7 +6,7 @@
 // workload: a `DotGeneral(x, w; lc=[1], rc=[1])` with a 2-D floating x and weight w becomes
 //
 //   sx = reduce_max(reduce_max(|x|, 1), 0) * (1/448)        (per-tensor, in-graph)
-//   xq = cast_e4m3(x * (1/sx))
+//   xq = cast_e4m3(x * (1/sx))       (1/1 when sx = 0: an all-zero x gives xq = 0 and y = 0)
 //   sw[n] = max_k |w[n,k]| / 448, wq = cast_e4m3(w / sw[n])  (per row; host-side when w is a Const,
 //                                                            from the stored f32 weight)
 //   y  = cast_out( dot(cast_f32(xq), cast_f32(wq)) * sx * sw[n] )
@@ -30,6 +30,13 @@ constexpr float kInv448 = 1.0f / 448.0f;
 namespace ku {
 
 namespace {
+
+// 1 / s where s > 0, else 1 / 1: an all-zero tensor (scale 0) then quantises to zeros, and its
+// product to zeros, instead of 0 * (1/0) = NaN.
+NodeId guarded_recip(Graph& g, NodeId s) {
+  NodeId pos = g.cmp_lt(g.scalar(s, 0.f), s);
+  return g.recip(g.where(pos, s, g.scalar(s, 1.f)));
+}
 
 double load_as_f64(DType dt, const uint8_t* p) {
   switch (dt) {
@@ -121,7 +128,7 @@ NodeId amp_fp8(Graph& g, NodeId root) {
         NodeId wa = g.max(wf, g.neg(wf));
         NodeId wm = g.reduce_max(wa, 1);
         sw_node = g.mul(wm, g.scalar(wm, kInv448));
-        NodeId inv = g.recip(sw_node);
+        NodeId inv = guarded_recip(g, sw_node);
         NodeId invb = g.broadcast_back(inv, {N, K}, 1);
         wq_node = g.cast(g.mul(wf, invb), DType::F8E4M3);
       }
@@ -131,7 +138,7 @@ NodeId amp_fp8(Graph& g, NodeId root) {
       NodeId rm = g.reduce_max(xa, 1);
       NodeId am = g.reduce_max(rm, 0);
       NodeId sx = g.mul(am, g.scalar(am, kInv448));
-      NodeId inv = g.recip(sx);
+      NodeId inv = guarded_recip(g, sx);
       NodeId invb = g.expand(g.reshape(inv, {1, 1}), {M, K});
       // The quantisation gets its own cast of x: the absmax pass and the quantise pass then each
       // read x in its own (16-bit) storage, instead of sharing an f32 copy written to HBM.

@@ -3,11 +3,20 @@
 Each graph starts from three constants (two matrices, one tensor of random rank) and grows by
 random steps drawn from the IR this backend runs: elementwise unary and binary ops, casts
 between float dtypes, movement (permute, reshape, slice with steps, flip, pad, broadcast),
-reductions (sum, max, softmax, and argmax of a constant), and f32 contractions. The last node
-and two random earlier ones are the roots, so one plan stores several outputs. Float graphs
+reductions (sum, max, softmax, and argmax of a constant), contractions and attention. The last
+node and two random earlier ones are the roots, so one plan stores several outputs. Float graphs
 draw values in [-4, 4]; integer graphs draw in [0, 8) so every op stays exact and in range in
 every integer dtype (the same spirit as kurumi_metal/src/tests/fuzz.rs:183-225, generated
 independently here).
+
+Contractions come in two kinds: small ones between matrices of the graph (f32 only), and ones
+with a contraction length that is a multiple of 64, in every float dtype, so that the 16-bit
+dtypes take the MFMA GEMM (plain, NT, batched, transposed lhs). Their operands are multiples of
+1/16 in [-1, 1]: every product and partial sum is then exact in f32 whatever the summation
+order, so the device and the oracle agree bit for bit on the contraction and it may feed any
+later op; every such contraction is also a root, so none is left unevaluated. Attention (fused or decomposed, causal or not, head sizes 32 / 64 / 128) takes q, k, v
+of the same kind; its result is not exact (exponentials), so it only ever becomes a root, and
+`attn_roots` lists those roots for a norm-wise bar.
 """
 from __future__ import annotations
 
@@ -76,16 +85,61 @@ def seed_shapes(rng, big: bool):
     return shapes
 
 
+def _sixteenths(g: Graph, rng, shape, dt: DType):
+    """A constant of multiples of 1/16 in [-1, 1] (exact in every float dtype)."""
+    vals = (rng.integers(-16, 17, int(np.prod(shape))) / 16.0).astype(np.float32)
+    node = g.constant_bytes(DType.F32, vals.tobytes(), list(shape))
+    return node if dt == DType.F32 else g.cast(node, dt)
+
+
+def _mfma_contraction(g: Graph, rng, dt: DType):
+    """A contraction of length 64, 128 or 192 in one of four layouts; returns (node, shape)."""
+    m, n, k = 1 + int(rng.integers(150)), 8 * (1 + int(rng.integers(40))), 64 * (1 + int(rng.integers(3)))
+    kind = int(rng.integers(4))
+    if kind == 0:  # [m, k] @ [k, n]
+        return g.matmul(_sixteenths(g, rng, [m, k], dt), _sixteenths(g, rng, [k, n], dt)), [m, n]
+    if kind == 1:  # [m, k] . [n, k]^T (the linear layout)
+        return g.dot_general(_sixteenths(g, rng, [m, k], dt), _sixteenths(g, rng, [n, k], dt), [1], [1]), [m, n]
+    if kind == 2:  # batched [b, m, k] @ [b, k, n]
+        b = 1 + int(rng.integers(3))
+        a, c = _sixteenths(g, rng, [b, m, k], dt), _sixteenths(g, rng, [b, k, n], dt)
+        return g.dot_general(a, c, [2], [1], [0], [0]), [b, m, n]
+    # transposed lhs: [k, m] contracted on its first axis
+    return g.dot_general(_sixteenths(g, rng, [k, m], dt), _sixteenths(g, rng, [k, n], dt), [0], [0]), [m, n]
+
+
+def _attention(g: Graph, rng, dt: DType):
+    b, h, s = 1 + int(rng.integers(2)), 1 + int(rng.integers(3)), 1 + int(rng.integers(200))
+    d = int(rng.choice([32, 64, 128]))
+    q, k, v = (_sixteenths(g, rng, [b, h, s, d], dt) for _ in range(3))
+    causal = bool(rng.integers(2))
+    f = g.sdpa_fused if rng.integers(2) else g.sdpa_decomposed
+    return f(q, k, v, causal)
+
+
 def float_graph(seed: int, dt: DType):
+    g, roots, _ = float_graph_info(seed, dt)
+    return g, roots
+
+
+def float_graph_info(seed: int, dt: DType):
+    """(graph, roots, attn_roots): attn_roots are the roots that are attention outputs."""
     rng = np.random.default_rng([seed, int(dt), 7])
     g = Graph()
     nodes = [(_const(g, rng, s, dt), s) for s in seed_shapes(rng, seed % 3 == 0)]
     leaves = list(nodes)
+    attn, mm = [], []
     for _ in range(8 + int(rng.integers(6))):
         node, shape = nodes[int(rng.integers(len(nodes)))]
-        k = int(rng.integers(7))
+        k = int(rng.integers(9))
         step = None
-        if k == 0:
+        if k == 7:
+            step = _mfma_contraction(g, rng, dt)
+            mm.append(step[0])
+        elif k == 8:
+            if len(attn) < 2:
+                attn.append(_attention(g, rng, dt))
+        elif k == 0:
             u = int(rng.integers(9))
             f = [g.neg, g.recip, g.sqrt, g.exp2, g.log2, g.sin, g.abs, g.floor, g.relu][u]
             step = (f(node), shape)
@@ -123,7 +177,7 @@ def float_graph(seed: int, dt: DType):
         if step is not None and step[1] and all(d > 0 for d in step[1]):
             nodes.append(step)
     roots = [nodes[-1][0]] + [nodes[int(rng.integers(len(nodes)))][0] for _ in range(2)]
-    return g, list(dict.fromkeys(roots))
+    return g, list(dict.fromkeys(roots + mm + attn)), set(attn)
 
 
 def int_graph(seed: int, dt: DType):

@@ -52,6 +52,31 @@ def interpret(g: Graph, roots, feeds: dict | None = None) -> list[Tensor]:
     return [Tensor._from_handle(out[i]) for i in range(len(roots))]
 
 
+def interpret_raw(g: Graph, roots, f: "K.Feeds") -> list[int]:
+    """The oracle interpreter alone, for timing: feeds bound beforehand (`K.Feeds`), outputs left
+    as handles in the oracle's memory (no copy out); release them with `free_raw`."""
+    roots = list(roots)
+    arr = (C.c_uint32 * len(roots))(*roots)
+    out = (C.c_void_p * len(roots))()
+    if oracle().kuo_interpret(g.h, arr, len(roots), f.h, out) != 0:
+        raise RuntimeError("oracle: " + oracle().kuo_last_error().decode())
+    return [out[i] for i in range(len(roots))]
+
+
+def realize_raw(g: Graph, root: int, f: "K.Feeds") -> list[int]:
+    """The view-fused evaluator alone, for timing (see `interpret_raw`)."""
+    out = C.c_void_p()
+    passes = C.c_int32()
+    if oracle().kuo_realize(g.h, root, f.h, C.byref(out), C.byref(passes)) < 0:
+        raise RuntimeError("oracle: " + oracle().kuo_last_error().decode())
+    return [out.value]
+
+
+def free_raw(handles: list[int]) -> None:
+    for h in handles:
+        K.lib().ku_tensor_free(h)
+
+
 def realize(g: Graph, root: int, feeds: dict | None = None) -> tuple[Tensor, int | None]:
     """View-fused CPU evaluator (restated realize::force); passes is None when it fell back."""
     f = K.Feeds(feeds or {})
@@ -133,9 +158,18 @@ def assert_close(got: np.ndarray, want: np.ndarray, rtol: float, atol: float, wh
     ok = (err <= atol + rtol * np.abs(want)) | both_nan | same_inf
     if not ok.all():
         i = np.argmax(~ok.reshape(-1))
-        raise AssertionError(f"{what}: {int((~ok).sum())} elements out of tolerance (rtol={rtol}, atol={atol}); "
-                             f"first at {np.unravel_index(i, got.shape)}: got {got.reshape(-1)[i]!r} "
+        a = np.broadcast_to(np.asarray(atol, dtype=np.float64), got.shape).reshape(-1)[i]
+        raise AssertionError(f"{what}: {int((~ok).sum())} elements out of tolerance (rtol={rtol}, atol at that "
+                             f"element={a!r}); first at {np.unravel_index(i, got.shape)}: got {got.reshape(-1)[i]!r} "
                              f"want {want.reshape(-1)[i]!r}")
+
+
+def bf16_ulp(x: np.ndarray) -> np.ndarray:
+    """Spacing of bf16 values at each |x| (8 significant bits): 2^(e-7) for |x| in [2^e, 2^(e+1)),
+    2^-133 below the smallest normal. Used as a per-element absolute floor for bf16 outputs."""
+    a = np.abs(np.asarray(x, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return np.exp2(e - 7)
 
 
 def rel_err(got: np.ndarray, want: np.ndarray) -> float:

@@ -72,6 +72,37 @@ def test_amp_leaves_non_f32_contractions_alone():
     assert K.amp(g, c) == c
 
 
+@pytest.mark.parametrize("weight", ["const", "input"])
+def test_amp_fp8_all_zero_operands_give_zeros_on_the_oracle(weight):
+    """The e4m3 pass divides by 1 where a scale is 0 (an all-zero activation, or an all-zero row
+    of an in-graph weight), so the product is 0 there instead of NaN; non-zero inputs are
+    quantised exactly as before (the guard passes sx through unchanged)."""
+    m, n, k = 4, 6, 128
+    rng = np.random.default_rng(2)
+    wv = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    wv[2] = 0.0  # an all-zero weight row
+    g = Graph()
+    x = g.input([m, k], DType.F32)
+    if weight == "const":
+        w = g.constant(wv)
+        feeds_w = {}
+    else:
+        w = g.input([n, k], DType.F32)
+        feeds_w = {w: Tensor.from_numpy(wv)}
+    y = K.amp_fp8(g, g.dot_general(x, w, [1], [1]))
+    zero = interpret(g, [y], {x: Tensor.from_numpy(np.zeros((m, k), np.float32)), **feeds_w})[0].numpy()
+    np.testing.assert_array_equal(zero, np.zeros((m, n), np.float32))
+    xv = rng.standard_normal((m, k)).astype(np.float32)
+    got = interpret(g, [y], {x: Tensor.from_numpy(xv), **feeds_w})[0].numpy()
+    assert np.isfinite(got).all() and (got[:, 2] == 0).all()
+    # the unguarded quantisation, restated with numpy: sx = max|x| / 448, xq = e4m3(x * (1/sx))
+    import kutest
+    sx = np.float32(np.abs(xv).max()) * np.float32(1.0 / 448.0)
+    xq = kutest.cast_bits((xv * (np.float32(1.0) / sx)).reshape(-1), DType.F32, DType.F8E4M3)
+    xq64 = kutest.cast_bits(xq, DType.F8E4M3, DType.F64).view(np.float64).reshape(m, k)
+    assert np.abs(got - (xq64 * np.float64(sx)) @ wv.astype(np.float64).T).max() <= 3e-2 * np.abs(got).max()
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
 def test_builders_on_device_match_oracle(hip, dt):

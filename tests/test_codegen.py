@@ -98,6 +98,43 @@ def test_decomposed_attention_with_non_causal_bias_is_not_matched():
     assert not any(x.startswith("attn") for x in st) and len(st) == 3
 
 
+def misplaced_causal_attention(g, s=64, d=32, dt=DType.F32):
+    """Scores [1, s, s, d] whose causal-valued constant is reshaped to [1, s, 1, s]: with H == S
+    the shapes line up, but the mask runs along (head, key) instead of (query, key)."""
+    q, k, v = (g.input([1, s, s, d], dt) for _ in range(3))
+    raw = g.dot_general(q, k, [3], [3], [0, 1], [0, 1])
+    sc = g.mul(raw, g.scalar(raw, 1.0 / np.sqrt(d)))
+    causal = np.triu(np.full((s, s), -np.inf, np.float32), 1)
+    bias = g.expand(g.reshape(g.constant(causal), [1, s, 1, s]), [1, s, s, s])
+    if dt != DType.F32:
+        bias = g.cast(bias, dt)
+    sc = g.add(sc, bias)
+    return (q, k, v), g.dot_general(g.softmax(sc, 3), v, [3], [2], [0, 1], [0, 1])
+
+
+@pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
+def test_decomposed_attention_with_misplaced_causal_bias_is_not_matched(dt):
+    g = Graph()
+    _, o = misplaced_causal_attention(g, dt=dt)
+    st = steps(g.codegen([o], compile=True))
+    assert not any(x.startswith("attn") for x in st), st
+
+
+def test_decomposed_attention_bias_with_other_expand_target_is_not_matched():
+    # bias broadcast to a larger shape than the scores (the add then broadcasts nothing): the
+    # expand target must equal the score shape exactly
+    g = Graph()
+    s = 64
+    q, k, v = (g.input([2, 1, s, 32], DType.F32) for _ in range(3))
+    raw = g.dot_general(q, k, [3], [3], [0, 1], [0, 1])
+    sc = g.mul(raw, g.scalar(raw, 0.125))
+    causal = np.triu(np.full((s, s), -np.inf, np.float32), 1)
+    sc = g.add(sc, g.expand(g.reshape(g.constant(causal), [1, 1, s, s]), [2, 1, s, s]))
+    o = g.dot_general(g.softmax(sc, 3), v, [3], [2], [0, 1], [0, 1])
+    st = steps(g.codegen([o]))
+    assert len(st) == 1 and st[0].startswith("attn") and "causal" in st[0]
+
+
 def test_cfg5_fp8_linear_lowering():
     g = Graph()
     x = g.input([2048, 4096], DType.BF16)

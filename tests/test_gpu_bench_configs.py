@@ -16,7 +16,7 @@ import pytest
 import bench
 import kurumi_amd as K
 from kurumi_amd import DType, Tensor
-from kutest import (assert_close, bf16_bits_to_f32, cast_bits, f32_to_bf16_bits, interpret, rel_err, to_f32)
+from kutest import (assert_close, bf16_bits_to_f32, bf16_ulp, cast_bits, f32_to_bf16_bits, interpret, rel_err, to_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -69,7 +69,8 @@ def test_cfg2_bench_plan_full_size(hip, dt_name):
     if dt_name == "f32":
         assert_close(y[rows], to_f32(wy), rtol=1e-4, atol=1e-30, what="softmax f32 vs oracle")
     else:
-        assert_close(y[rows], to_f32(wy), rtol=1e-2, atol=1e-2 * to_f32(wy).max(), what="softmax bf16 vs oracle")
+        want = to_f32(wy)  # elementwise: 1e-2 of each element plus one bf16 step at its magnitude
+        assert_close(y[rows], want, rtol=1e-2, atol=bf16_ulp(want), what="softmax bf16 vs oracle")
 
 
 # ---------------- config 1 ----------------
@@ -107,6 +108,17 @@ def test_cfg3_bench_plan_full_size(hip):
     truth = A[rows] @ B
     assert rel_err(got[rows], truth) <= 1e-2
     assert_close(got[rows], truth, rtol=1e-2, atol=1e-2 * np.abs(truth).max(), what="cfg3 vs f64")
+    # the oracle (f32 GEMM of the bf16 inputs, rounded once to bf16) on 16 of those rows: both
+    # round an f32 sum of the same products, so they agree to a bf16 step except where the f32
+    # sums' different orders straddle a rounding boundary near zero
+    orows = np.concatenate([rows[:4], rows[len(rows) // 2 - 4:len(rows) // 2 + 4], rows[-4:]])
+    g = K.Graph()
+    a = g.input([len(orows), 4096], DType.BF16)
+    b = g.input([4096, 11008], DType.BF16)
+    y = g.matmul(a, b)
+    abits = np.ascontiguousarray(c.feeds[c.a].numpy()[orows])
+    want = to_f32(interpret(g, [y], {a: Tensor(DType.BF16, [len(orows), 4096], abits.tobytes()), b: c.feeds[c.b]})[0])
+    assert_close(got[orows], want, rtol=1e-2, atol=bf16_ulp(want) + 1e-4 * np.abs(want).max(), what="cfg3 vs oracle")
 
 
 def test_cfg3b_bench_plan_full_size(hip):

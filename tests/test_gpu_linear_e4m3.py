@@ -71,6 +71,29 @@ def test_linear_e4m3_dtypes(hip, x_dtype, y_dtype):
     assert_close(gf, truth, rtol=3e-2, atol=3e-2 * np.abs(truth).max(), what="linear_e4m3 dtypes")
 
 
+def test_linear_e4m3_all_zero_activation_gives_zeros(hip):
+    """sx = max|x| / 448 = 0: both the entry point and the graph path divide by 1 instead, so
+    xq = 0 and y = 0 (not 0 * inf = NaN), and they still agree bit for bit."""
+    m, n, k = 64, 256, 256
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((n, k), dtype=np.float32) * 0.02).astype(np.float32)
+    xbits = np.zeros((m, k), np.uint16)
+    wq, sw = quantise_rows(w)
+    got = run_direct(hip, xbits, DType.BF16, wq, sw, DType.BF16, m, n, k)
+    np.testing.assert_array_equal(got, np.zeros((m, n), np.uint16))
+    g, x, y = bench.fp8_graph(K, [m, k], w.tobytes(), [n, k])
+    plan = hip.plan(g, [y], {x: Tensor(DType.BF16, [m, k], xbits.tobytes())})
+    assert plan.steps()[0].startswith("actq_e4m3"), plan.steps()
+    plan.launch()
+    np.testing.assert_array_equal(plan.output(0).numpy(), got)
+    # and a non-zero x afterwards on the same buffers' path still matches the graph
+    xbits = f32_to_bf16_bits(rng.standard_normal((m, k), dtype=np.float32))
+    got = run_direct(hip, xbits, DType.BF16, wq, sw, DType.BF16, m, n, k)
+    plan.feed(x, Tensor(DType.BF16, [m, k], xbits.tobytes()))
+    plan.launch()
+    np.testing.assert_array_equal(plan.output(0).numpy(), got)
+
+
 def test_linear_e4m3_rejects_bad_arguments(hip):
     d = DevBuf(4096)
     with pytest.raises(K.KuError, match="multiple of 128"):

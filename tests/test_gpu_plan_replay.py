@@ -138,6 +138,44 @@ def test_process_using_ku_plan_exits_cleanly():
     assert r.returncode == 0 and "ran" in r.stdout, (r.returncode, r.stdout, r.stderr[-2000:])
 
 
+def test_plans_outlive_the_backend_handle_they_were_built_on():
+    """ku_backend_free before ku_plan_free / ku_hip_plan_free: the plans keep the backend (its
+    stream, pools and constant cache) alive, run correctly after the handle is gone, and the
+    process exits cleanly once the last plan is freed."""
+    code = textwrap.dedent(f"""
+        import ctypes as C, sys
+        sys.path.insert(0, {str(ROOT)!r})
+        import numpy as np
+        import kurumi_amd as K
+        L = K.lib()
+        g = K.Graph()
+        x = g.input([16, 300], K.DType.F32)
+        w = g.constant(np.linspace(-1, 1, 300 * 64, dtype=np.float32).reshape(300, 64))
+        y = g.softmax(g.matmul(x, w), 1)
+        xv = np.random.default_rng(3).standard_normal((16, 300)).astype(np.float32)
+        feeds = K.Feeds({{x: K.Tensor.from_numpy(xv)}})
+        ref = K.HipBackend()
+        want = ref.eval_with(g, y, {{x: K.Tensor.from_numpy(xv)}}).numpy()
+        b = L.ku_backend_new(2)
+        assert b
+        p = L.ku_hip_plan_compile_on(b, g.h, y)
+        roots = (C.c_uint32 * 1)(y)
+        hp = L.ku_hip_plan_new(g.h, roots, 1, b, feeds.h)
+        assert p and hp
+        L.ku_backend_free(b)
+        print("backend handle freed", flush=True)
+        t = K.Tensor._from_handle(L.ku_plan_run(p, g.h, feeds.h))
+        np.testing.assert_array_equal(t.numpy(), want)
+        assert L.ku_hip_plan_launch(hp, 1) == 0 and L.ku_hip_plan_sync(hp) == 0
+        np.testing.assert_array_equal(K.Tensor._from_handle(L.ku_hip_plan_output(hp, 0)).numpy(), want)
+        L.ku_plan_free(p)
+        L.ku_hip_plan_free(hp)
+        print("ran", flush=True)
+    """)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "ran" in r.stdout, (r.returncode, r.stdout, r.stderr[-2000:])
+
+
 def test_equal_graphs_from_one_blob_share_plan_and_constants(hip):
     """The KGPH seam decodes a fresh graph per call: the second decode finds the first's plan and
     weights by content (no new plan, no new constant upload), and results stay identical."""

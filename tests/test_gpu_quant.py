@@ -170,6 +170,76 @@ def test_quant_constant_weight_shared_by_plans(hip):
         check(m)
 
 
+@pytest.mark.parametrize("sym", [True, False])
+@pytest.mark.parametrize("m,n", [(17, 99), (40, 35)])
+def test_quant_mfma_odd_group_count_and_rows(hip, m, n, sym):
+    """The fused MFMA kernel with an odd number of scale groups per row (k / group = 3) and an odd
+    row count in the last work-group's tile: the table's last scale (and min) shares a dword
+    with the row past N, and must still be read."""
+    print(f"quant mfma odd ng m={m} n={n} sym={sym}", flush=True)
+    g, x, y, xt, truth = build(m, n, 384, 4, 128, sym, DType.BF16, 900 + m + n)
+    plan = hip.plan(g, [y], {x: xt})
+    assert plan.steps()[0].startswith("quant_mfma"), plan.steps()
+    got = to_f32(hip.eval_with(g, y, {x: xt}))
+    want = to_f32(interpret(g, [y], {x: xt})[0])
+    assert rel_err(got, truth) <= 1e-2, rel_err(got, truth)
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="odd-ng quant mfma vs oracle")
+    # the last row's last group alone: its scale must not read as 0
+    assert np.abs(got[:, -1] - want[:, -1]).max() <= 1e-2 * np.abs(want).max()
+
+
+def test_quant_constant_weight_read_at_two_shapes(hip):
+    """One packed int4 constant read as [256, 1024] and, reshaped, as [512, 512] (each packed row
+    split in two, its scale row with it). The constant's cache entry keeps one lane-ordered copy
+    per shape, so neither read loses its copy to the other: within one plan, and across two plans
+    that share the constant by content, every output matches the oracle, also when the first
+    plan is launched again after the second was built."""
+    n, k, group, m = 256, 1024, 128, 32
+    rng = np.random.default_rng(43)
+    w = rng.standard_normal((n, k)).astype(np.float32)
+    p, s, _ = K.quantize(w, 4, group, True)
+
+    def graph(shapes):
+        g = Graph()
+        qw = g.constant_bytes(DType.U8, p.tobytes(), p.shape)
+        sc = g.constant_bytes(DType.F16, s.tobytes(), s.shape)
+        ins, outs = [], []
+        for rows in shapes:  # rows of the weight it is read as: n or 2n
+            kk = n * k // rows
+            x = g.input([m, kk], DType.BF16)
+            q = qw if rows == n else g.reshape(qw, [rows, kk // 2])
+            c = sc if rows == n else g.reshape(sc, [rows, kk // group])
+            ins.append(x)
+            outs.append(g.quant_matmul(x, q, c, None, 4, group))
+        return g, ins, outs
+
+    acts = {rows: interpret(*(lambda gg: (gg, [gg.cast(gg.constant(
+        rng.standard_normal((m, n * k // rows)).astype(np.float32)), DType.BF16)]))(Graph()))[0] for rows in (n, 2 * n)}
+
+    def check(plan, g, ins, outs, shapes, what):
+        plan.launch()
+        plan.sync()
+        feeds = {x: acts[rows] for x, rows in zip(ins, shapes)}
+        wants = interpret(g, outs, feeds)
+        for i, rows in enumerate(shapes):
+            got, want = to_f32(plan.output(i)), to_f32(wants[i])
+            assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what=f"{what} rows={rows}")
+
+    # one plan, both shapes
+    g, ins, outs = graph([n, 2 * n])
+    plan = hip.plan(g, outs, {ins[0]: acts[n], ins[1]: acts[2 * n]})
+    assert all(st.startswith("quant_mfma") for st in plan.steps()), plan.steps()
+    check(plan, g, ins, outs, [n, 2 * n], "one plan")
+    # two plans sharing the constant
+    ga, ia, oa = graph([n])
+    pa = hip.plan(ga, oa, {ia[0]: acts[n]})
+    gb, ib, ob = graph([2 * n])
+    pb = hip.plan(gb, ob, {ib[0]: acts[2 * n]})
+    check(pb, gb, ib, ob, [2 * n], "second plan")
+    check(pa, ga, ia, oa, [n], "first plan after the second")
+    check(plan, g, ins, outs, [n, 2 * n], "one plan again")
+
+
 def test_quant_mfma_batched_decode_size(hip):
     """A batch of 32 tokens through the int4 (group 128) [11008, 4096] projection."""
     print("quant mfma 32x4096 -> 11008", flush=True)
