@@ -280,10 +280,14 @@ attn_mfma_k(AttnArgs a) {
       // the two halves of the wave hold the same queries: exchange without LDS
       const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(bm), __float_as_uint(bm), false, false);
       bm = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * c;
-      // both halves see the same bm and mc, so they take the same decision
-      if (__builtin_amdgcn_ballot_w64(bm > mc[u] + RESCALE) != 0) {
-        const float mn = fmaxf(mc[u], bm);
-        const float corr = __builtin_amdgcn_exp2f(mc[u] - mn);
+      // Each query decides for itself (both halves of the wave see the same bm and mc, so they
+      // agree): a query that keeps its max multiplies by exactly 1. A query's result thus depends
+      // on its own scores alone, never on a neighbour's rescale; the branch is skipped when no
+      // query of the wave needs it.
+      const bool need = bm > mc[u] + RESCALE;
+      if (__builtin_amdgcn_ballot_w64(need) != 0) {
+        const float mn = need ? fmaxf(mc[u], bm) : mc[u];
+        const float corr = need ? __builtin_amdgcn_exp2f(mc[u] - mn) : 1.f;
         mc[u] = mn;
         l[u] *= corr;
 #pragma unroll
