@@ -152,18 +152,38 @@ attn_mfma_k(AttnArgs a) {
   const int64_t ntiles = (int64_t)nqt * bh;
   const int64_t G = gridDim.x;
   const uint32_t hb = (uint32_t)(S * D * 2);  // bytes per head
-  // Tile t is head t % bh, q-tile t / bh (causal: heaviest first). Work-group b takes tile
-  // r*G + b in round r, and in odd rounds the tile at the mirrored position among the
+  // Otherwise tile t is head t % bh, q-tile t / bh (causal: heaviest first). Work-group b takes
+  // tile r*G + b in round r, and in odd rounds the tile at the mirrored position among the
   // work-groups of its XCD (b % 8 kept): the causal tiles' sizes even out over a work-group's
-  // rounds, and with bh % 8 == 0 every tile of a head runs on one XCD, whose L2 keeps its K / V.
+  // rounds, and with bh % 8 == 0 every tile of a head runs on one XCD.
+  // Head-grouped order (when the shapes allow it): round r runs every q-tile of G / nqt heads,
+  // each XCD (b % 8) G / nqt / 8 of them, so the q-tiles of a head start their walks over its
+  // K / V blocks together and read them from one L2 (cfg 4: fetched bytes -28 %); in odd rounds
+  // a work-group takes the mirrored q-tile, which evens out the causal tiles' sizes over two
+  // rounds.
+  const bool grouped = (G % (8 * (int64_t)nqt)) == 0 && bh % (G / nqt) == 0;
   auto tile_at = [&](int r) {
     const int64_t b = blockIdx.x;
-    const bool mirror = (r & 1) && (G & 7) == 0;
-    const int64_t t = (int64_t)r * G + (mirror ? (b & 7) + 8 * (G / 8 - 1 - (b >> 3)) : b);
     Tile T{0, S, 0, 0};
-    if (t < ntiles) {
-      const int ti = (int)t, qt = a.causal ? nqt - 1 - ti / bh : ti / bh;
-      T.head = ti % bh;
+    int head = 0, qt = 0;
+    bool valid;
+    if (grouped) {
+      const int64_t hpr = G / nqt, hpx = hpr / 8, x = b & 7, j = b >> 3, qs = j % nqt;
+      valid = (int64_t)r * hpr < bh;
+      head = (int)(r * hpr + x * hpx + j / nqt);
+      qt = (int)((r & 1) ? nqt - 1 - qs : qs);
+    } else {
+      const bool mirror = (r & 1) && (G & 7) == 0;
+      const int64_t t = (int64_t)r * G + (mirror ? (b & 7) + 8 * (G / 8 - 1 - (b >> 3)) : b);
+      valid = t < ntiles;
+      if (valid) {
+        const int ti = (int)t;
+        qt = a.causal ? nqt - 1 - ti / bh : ti / bh;
+        head = ti % bh;
+      }
+    }
+    if (valid) {
+      T.head = head;
       T.q0 = qt * BQ;
       const int kend = a.causal ? (T.q0 + BQ < S ? T.q0 + BQ : S) : S;  // keys the tile needs
       T.nkv = (kend + BK - 1) / BK;
