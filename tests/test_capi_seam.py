@@ -14,6 +14,7 @@ import textwrap
 from pathlib import Path
 
 import numpy as np
+import pytest
 
 import kurumi_amd as K
 from kurumi_amd import DType, Graph
@@ -57,6 +58,12 @@ size_t ku_tensor_nbytes(const void *t) { calls++; return 77; }
 void ku_tensor_bytes(const void *t, uint8_t *o) { calls++; }
 size_t ku_node_count(const void *g, uint32_t r) { calls++; return 77; }
 size_t ku_dump(const void *g, uint32_t r, uint8_t *o, size_t c) { calls++; return 77; }
+void *ku_eval(void *g, uint32_t n, const void *b) { calls++; return (void *)0x5157; }
+void *ku_eval_with(void *g, uint32_t n, const void *b, const void *f) { calls++; return (void *)0x5158; }
+int32_t ku_eval_many(void *g, const uint32_t *ids, size_t n, const void *b, const void *f, void **out) { calls++; return 0; }
+void *ku_hip_plan_compile_on(const void *b, const void *g, uint32_t n) { calls++; return (void *)0x5159; }
+void *ku_plan_run(const void *p, const void *g, const void *f) { calls++; return (void *)0x515a; }
+void ku_plan_free(void *p) { calls++; }
 """
 
 # Field order of KuHipApi in include/kurumi_hip.h (after version and size).
@@ -173,3 +180,80 @@ def test_table_matches_the_exported_definitions():
     for i, f in enumerate(FIELDS):
         name = {"plan_compile_on": "ku_hip_plan_compile_on"}.get(f, "ku_" + f)
         assert ptrs[i] == C.cast(getattr(L, name), C.c_void_p).value, f
+
+
+# The backend seam on the device: a KGPH blob evaluated on KU_HIP, and planned and replayed,
+# entirely through the table, with the same-named stand-in loaded first.
+GPU_CHILD = textwrap.dedent(r"""
+    import ctypes as C, json, sys
+    import numpy as np
+    standin_path, lib_path, blob_path, x_path = sys.argv[1:5]
+    S = C.CDLL(standin_path, mode=C.RTLD_GLOBAL)
+    L = C.CDLL(lib_path, mode=C.RTLD_GLOBAL)
+    FIELDS, F32 = json.loads(sys.argv[5]), int(sys.argv[6])
+    P, Z, U32 = C.c_void_p, C.c_size_t, C.c_uint32
+    class Api(C.Structure):
+        _fields_ = [("version", U32), ("size", U32)] + [(f, P) for f in FIELDS]
+    L.ku_hip_api.restype = C.POINTER(Api)
+    T = L.ku_hip_api(1).contents
+    fn = lambda name, res, *args: C.CFUNCTYPE(res, *args)(getattr(T, name))
+    b = fn("backend_new", P, U32)(2)
+    assert b, fn("last_error", C.c_char_p)()
+    blob = open(blob_path, "rb").read()
+    r = fn("graph_deserialize", P, C.c_char_p, Z)(blob, len(blob))
+    outs = [fn("runnable_output", U32, P, Z)(r, i) for i in range(fn("runnable_output_count", Z, P)(r))]
+    xin = fn("runnable_input_node", U32, P, Z)(r, 0)
+    g = fn("runnable_take_graph", P, P)(r)
+    fn("runnable_free", None, P)(r)
+    x = np.load(x_path)
+    shape = (Z * 2)(*x.shape)
+    t = fn("tensor_new", P, U32, P, Z, P, Z)(F32, x.ctypes.data, x.nbytes, C.addressof(shape), 2)
+    f = fn("feeds_new", P)()
+    fn("feeds_set", None, P, U32, P)(f, xin, t)
+    ids = (U32 * len(outs))(*outs)
+    res = (P * len(outs))()
+    assert fn("eval_many", C.c_int32, P, P, Z, P, P, P)(g, ids, len(outs), b, f, res) == 0, fn("last_error", C.c_char_p)()
+    def fetch(h):
+        n = fn("tensor_nbytes", Z, P)(h)
+        buf = (C.c_uint8 * n)()
+        fn("tensor_bytes", None, P, P)(h, buf)
+        fn("tensor_free", None, P)(h)
+        return bytes(buf).hex()
+    got = [fetch(res[i]) for i in range(len(outs))]
+    p = fn("plan_compile_on", P, P, P, U32)(b, g, outs[0])
+    assert p, fn("last_error", C.c_char_p)()
+    replay = fetch(fn("plan_run", P, P, P, P)(p, g, f))
+    fn("plan_free", None, P)(p)
+    fn("feeds_free", None, P)(f)
+    fn("tensor_free", None, P)(t)
+    fn("graph_free", None, P)(g)
+    fn("backend_free", None, P)(b)
+    S.standin_calls.restype = C.c_int
+    print(json.dumps({"got": got, "replay": replay, "standin_calls": S.standin_calls()}))
+""")
+
+
+@pytest.mark.gpu
+def test_table_evaluates_and_replays_on_the_gpu_with_same_names_loaded_first(hip, tmp_path):
+    src = tmp_path / "standin.c"
+    src.write_text(STANDIN)
+    standin = tmp_path / "libstandin.so"
+    subprocess.run(["gcc", "-shared", "-fPIC", "-O1", "-o", str(standin), str(src)], check=True)
+    g = Graph()
+    x = g.input([64, 1000], DType.F32)
+    y = g.softmax(x, 1)
+    a = g.cast(g.argmax(y, 1), DType.I32)
+    blob = tmp_path / "g.kgph"
+    blob.write_bytes(K.serialize_graph(g, [y, a], [K.InputBinding(x, K.InputRole.Runtime, "x")]))
+    xv = np.random.default_rng(4).standard_normal((64, 1000)).astype(np.float32) * 3
+    np.save(tmp_path / "x.npy", xv)
+    # the same graph through the plain names, in this process (no stand-in here)
+    want = hip.eval_many_with(g, [y, a], {x: K.Tensor.from_numpy(xv)})
+    r = subprocess.run([sys.executable, "-c", GPU_CHILD, str(standin), str(LIB), str(blob), str(tmp_path / "x.npy"),
+                        json.dumps(FIELDS), str(int(DType.F32))], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr[-3000:]
+    out = json.loads(r.stdout.strip().splitlines()[-1])
+    assert out["standin_calls"] == 0
+    assert bytes.fromhex(out["got"][0]) == want[0].numpy().tobytes()
+    assert bytes.fromhex(out["got"][1]) == want[1].numpy().tobytes()
+    assert bytes.fromhex(out["replay"]) == want[0].numpy().tobytes()
