@@ -7,11 +7,13 @@
 #include <unistd.h>
 
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <sstream>
+#include <thread>
 
 namespace ku::hipbk {
 
@@ -101,7 +103,7 @@ static void mkdirs(const std::string& path) {
   }
 }
 
-std::vector<char> rtc_compile(const std::string& src, const std::string& name_hint) {
+std::vector<char> rtc_compile(const std::string& src, const std::string& name_hint, bool fresh) {
   std::string key;
   for (int i = 0; i < kNumRtcOpts; ++i) key += kRtcOpts[i], key += ' ';
   int ver_major = 0, ver_minor = 0;
@@ -112,7 +114,7 @@ std::vector<char> rtc_compile(const std::string& src, const std::string& name_hi
   bool use_disk = !std::getenv("KURUMI_HIP_NO_DISK_CACHE");
   std::string dir = rtc_cache_dir();
   std::string path = dir + "/" + hex + ".co";
-  if (use_disk) {
+  if (use_disk && !fresh) {
     std::ifstream f(path, std::ios::binary);
     if (f) {
       std::vector<char> co((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
@@ -137,13 +139,22 @@ std::vector<char> rtc_compile(const std::string& src, const std::string& name_hi
   hiprtcGetCode(prog, co.data());
   hiprtcDestroyProgram(&prog);
   if (use_disk) {
+    // Each writer its own temporary (backends in several threads, or processes, may compile the
+    // same source at once) and an atomic rename, so a reader sees a whole file or none; a failed
+    // or short write is never renamed into place.
+    static std::atomic<uint64_t> seq{0};
     mkdirs(dir);
-    std::string tmp = path + ".tmp" + std::to_string(::getpid());
+    const std::string tmp = path + ".tmp" + std::to_string(::getpid()) + "." +
+                            std::to_string(std::hash<std::thread::id>{}(std::this_thread::get_id())) + "." +
+                            std::to_string(seq.fetch_add(1));
+    bool ok;
     {
       std::ofstream f(tmp, std::ios::binary);
       f.write(co.data(), static_cast<std::streamsize>(co.size()));
+      f.close();
+      ok = !f.fail();
     }
-    std::rename(tmp.c_str(), path.c_str());
+    if (!ok || std::rename(tmp.c_str(), path.c_str()) != 0) std::remove(tmp.c_str());
   }
   return co;
 }
@@ -156,7 +167,13 @@ KernelFn ModuleCache::get(const std::string& src, const std::string& entry) {
   }
   std::vector<char> co = rtc_compile(src, entry);
   KernelFn k;
-  KU_HIP(hipModuleLoadData(&k.mod, co.data()));
+  if (hipModuleLoadData(&k.mod, co.data()) != hipSuccess) {
+    // a code object from the disk cache that does not load (damaged on disk): compile afresh,
+    // which also replaces the cached file
+    (void)hipGetLastError();
+    co = rtc_compile(src, entry, /*fresh=*/true);
+    KU_HIP(hipModuleLoadData(&k.mod, co.data()));
+  }
   KU_HIP(hipModuleGetFunction(&k.fn, k.mod, entry.c_str()));
   ++compiled_;
   map_.emplace(src, k);

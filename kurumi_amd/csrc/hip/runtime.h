@@ -58,8 +58,9 @@ struct KernelFn {
 };
 
 // Compile generated HIP source for gfx950 with hipRTC; cache code objects in memory
-// (by source) and on disk (by a hash of source + options) so a re-run skips the compile.
-std::vector<char> rtc_compile(const std::string& src, const std::string& name_hint);
+// (by source) and on disk (by a hash of source, options and hipRTC version) so a re-run skips
+// the compile. fresh = true ignores the disk copy (and rewrites it).
+std::vector<char> rtc_compile(const std::string& src, const std::string& name_hint, bool fresh = false);
 std::string rtc_cache_dir();
 
 class ModuleCache {
