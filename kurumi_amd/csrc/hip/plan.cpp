@@ -1731,6 +1731,21 @@ Plan::Plan(const Graph& g, const std::vector<NodeId>& roots, Context* ctx, Const
   for (NodeId r : roots_) root_meta_.push_back({g.dtype(r), g.shape(r)});
   compile();
   if (ctx_) {
+    try {
+      bind_device_buffers(g, consts);
+    } catch (...) {
+      // the destructor does not run for a constructor that throws: give this plan's buffers
+      // back to the pool (an allocation that failed on a full device must not leak the others)
+      for (auto& sl : slots_)
+        if (!sl.borrowed && sl.buf.ptr) ctx_->pool().release(sl.buf);
+      throw;
+    }
+  }
+  bg_ = nullptr;
+}
+
+void Plan::bind_device_buffers(const Graph& g, ConstCache* consts) {
+  {
     allocate();
     std::map<int, ConstEntry*> const_of;  // slot -> its cache entry
     for (size_t i = 0; i < slots_.size(); ++i) {
@@ -1758,7 +1773,6 @@ Plan::Plan(const Graph& g, const std::vector<NodeId>& roots, Context* ctx, Const
         Q.qw_tiled = it->second.ptr;
       }
   }
-  bg_ = nullptr;
 }
 
 Plan::~Plan() {

@@ -211,6 +211,8 @@ class Plan {
   friend class Planner;
   void compile();
   void allocate();
+  // device buffers of the slots, the constants from the cache and their lane-ordered copies
+  void bind_device_buffers(const Graph& g, ConstCache* consts);
   void launch_step(const Step& s);
 
   const Graph* bg_ = nullptr;  // the graph being planned; valid during construction only

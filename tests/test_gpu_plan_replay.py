@@ -203,3 +203,39 @@ def test_equal_graphs_from_one_blob_share_plan_and_constants(hip):
     third = hip.eval_with(g3, y3, {x3: feeds_v})
     assert hip.profile()["plans_built"] == after["plans_built"] + 1
     assert not np.array_equal(third.numpy(), first.numpy())
+
+
+def test_a_plan_that_runs_out_of_device_memory_gives_its_buffers_back():
+    """A device plan whose buffers do not fit (102 GB + 256 GB outputs on a 288 GB GPU) fails with
+    an error naming the failed allocation, and the backend gets back what that plan had already
+    allocated: a 205 GB plan on the same backend then fits (it would not beside a leaked 102 GB).
+    Run in a child process so nothing it holds can crowd the other tests."""
+    code = textwrap.dedent(f"""
+        import sys
+        sys.path.insert(0, {str(ROOT)!r})
+        import numpy as np
+        import kurumi_amd as K
+        be = K.HipBackend()
+
+        def big(rows_list):
+            g = K.Graph()
+            x = g.input([1, 1024], K.DType.F32)
+            ys = [g.expand(g.mul(x, g.scalar(x, float(i + 2))), [r, 1024]) for i, r in enumerate(rows_list)]
+            return g, x, ys
+
+        g, x, ys = big([25_000_000, 62_500_000])
+        feeds = {{x: K.Tensor.from_numpy(np.ones((1, 1024), np.float32))}}
+        try:
+            K.HipPlan(be, g, ys, feeds)
+            raise SystemExit("the 358 GB plan was built")
+        except K.KuError as e:
+            msg = str(e)
+        assert "hipMalloc" in msg or "memory" in msg.lower(), msg
+        print("failed as expected:", msg.splitlines()[0][:160], flush=True)
+        g2, x2, ys2 = big([50_000_000])
+        p = K.HipPlan(be, g2, ys2, {{x2: K.Tensor.from_numpy(np.ones((1, 1024), np.float32))}})
+        del p
+        print("ran", flush=True)
+    """)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "ran" in r.stdout, (r.returncode, r.stdout, r.stderr[-2000:])
