@@ -238,6 +238,40 @@ def test_attention_persistent_work_groups_match_oracle(hip, monkeypatch, grid, d
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="attention")
 
 
+def _attn_grouped_rounds(shape, grid):
+    """Rounds of the head-grouped tile order the MFMA kernel takes at this shape and capped grid
+    (0 when the shape does not meet its conditions). Mirrors the launcher (grids of whole XCD
+    groups) and the kernel's test: grid % (8 * q-tiles) == 0 and heads % (grid / q-tiles) == 0."""
+    bh, s = shape[0] * shape[1], shape[2]
+    nqt = (s + 127) // 128
+    g = min(nqt * bh, grid)
+    if g < nqt * bh:
+        g = max(8, g & ~7)
+    if g % (8 * nqt) or bh % (g // nqt):
+        return 0
+    return bh // (g // nqt)
+
+
+@pytest.mark.parametrize("dt,causal,shape,grid", [(DType.BF16, True, [2, 8, 256, 128], 16),
+                                                  (DType.F16, True, [2, 8, 256, 64], 16),
+                                                  (DType.BF16, True, [1, 16, 384, 64], 24),
+                                                  (DType.BF16, False, [1, 24, 200, 128], 16)])
+def test_attention_head_grouped_order_matches_oracle(hip, monkeypatch, dt, causal, shape, grid):
+    # the tile order cfg 4 runs at full size (every q-tile of a head on one XCD in the same round,
+    # odd rounds taking the mirrored q-tile), at small shapes with two and three rounds
+    rounds = _attn_grouped_rounds(shape, grid)
+    assert rounds >= 2, "shape/grid must take the head-grouped order over several rounds"
+    print(f"attention head-grouped grid={grid} rounds={rounds} dt={dt} causal={causal} shape={shape}", flush=True)
+    monkeypatch.setenv("KURUMI_HIP_ATTN_GRID", str(grid))
+    g, q, k, v, o = attention_graph(shape, dt, causal, True)
+    mk = f16_tensor if dt == DType.F16 else bf16_tensor
+    feeds = {q: mk(randn(shape, 71)), k: mk(randn(shape, 72)), v: mk(randn(shape, 73))}
+    assert "attn_mfma" in hip.plan(g, [o], feeds).steps()[0]
+    got = to_f32(hip.eval_with(g, o, feeds))
+    want = to_f32(interpret(g, [o], feeds)[0])
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="attention (head-grouped order)")
+
+
 def test_attention_full_size_mfma_agrees_with_rowwise_kernel(hip, monkeypatch):
     # cfg 4 at its real shape: the MFMA flash kernel against the independent one-query-per-thread
     # kernel (f32 dot products, no MFMA), which the small-shape tests pin to the oracle
