@@ -289,6 +289,24 @@ def test_attention_full_size_mfma_agrees_with_rowwise_kernel(hip, monkeypatch):
     assert_close(fast, slow, rtol=1e-2, atol=1e-2 * np.abs(slow).max(), what="attention mfma vs rowwise")
 
 
+@pytest.mark.parametrize("dt,causal,shape", [(DType.BF16, True, [1, 8, 8192, 128]), (DType.F16, False, [1, 4, 6000, 64])])
+def test_attention_long_sequence_mfma_agrees_with_rowwise_kernel(hip, monkeypatch, dt, causal, shape):
+    # long rows: a q-tile walks up to 64 key blocks (lazy rescale over many blocks, the pipeline
+    # across long tiles), checked against the one-query-per-thread kernel (f32, no MFMA)
+    print(f"attention long sequence dt={dt} causal={causal} shape={shape}", flush=True)
+    g, q, k, v, o = attention_graph(shape, dt, causal, True)
+    rng = np.random.default_rng(11)
+    mk = f16_tensor if dt == DType.F16 else bf16_tensor
+    feeds = {n: mk(rng.standard_normal(shape, dtype=np.float32)) for n in (q, k, v)}
+    assert "attn_mfma" in hip.plan(g, [o], feeds).steps()[0]
+    fast = to_f32(hip.eval_with(g, o, feeds))
+    monkeypatch.setenv("KURUMI_HIP_NO_MFMA", "1")
+    g2, q2, k2, v2, o2 = attention_graph(shape, dt, causal, True)
+    slow = to_f32(hip.eval_with(g2, o2, {q2: feeds[q], k2: feeds[k], v2: feeds[v]}))
+    assert np.isfinite(fast).all()
+    assert_close(fast, slow, rtol=1e-2, atol=1e-2 * np.abs(slow).max(), what="attention long sequence mfma vs rowwise")
+
+
 def test_attention_causal_prefix_invariance(hip):
     # causality: changing keys/values after position p leaves outputs of queries <= p bit-identical
     shape, p = [1, 4, 1024, 128], 700
