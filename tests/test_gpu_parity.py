@@ -171,6 +171,25 @@ def test_gemm_layouts_and_edges_match_oracle(hip, dt, nt, m, k, n):
     assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="gemm layout")
 
 
+@pytest.mark.parametrize("dt,nt", [(DType.BF16, False), (DType.F16, True)])
+def test_gemm_long_contraction_matches_f64(hip, dt, nt):
+    # K = 32768 (512 stages of the MFMA loop) with tiles cut by M and N; the reference is the f64
+    # product of the same rounded inputs (the oracle's sequential f32 fold is too slow here)
+    m, k, n = 300, 32768, 520
+    print(f"gemm long K {dt.name} nt={nt} {m}x{k}x{n}", flush=True)
+    g = Graph()
+    a = g.input([m, k], dt)
+    b = g.input([n, k] if nt else [k, n], dt)
+    c = g.dot_general(a, b, [1], [1] if nt else [0])
+    mk = f16_tensor if dt == DType.F16 else bf16_tensor
+    feeds = {a: mk(randn([m, k], 37, 1.0 / 64)), b: mk(randn([n, k] if nt else [k, n], 38, 1.0 / 4))}
+    assert "gemm_mfma" in hip.plan(g, [c], feeds).steps()[0]
+    got = to_f32(hip.eval_with(g, c, feeds))
+    a64, b64 = to_f32(feeds[a]).astype(np.float64), to_f32(feeds[b]).astype(np.float64)
+    want = a64 @ (b64.T if nt else b64)
+    assert_close(got, want, rtol=1e-2, atol=1e-2 * np.abs(want).max(), what="gemm long K")
+
+
 def test_cfg3_batched_gemm_matches_oracle(hip):
     g = Graph()
     a = g.input([4, 256, 128], DType.BF16)
