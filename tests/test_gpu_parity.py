@@ -82,8 +82,9 @@ def softmax_graph(rows: int, cols: int, dt: DType, decomposed: bool):
 
 @pytest.mark.parametrize("dt", [DType.F32, DType.BF16])
 @pytest.mark.parametrize("decomposed", [False, True])
-@pytest.mark.parametrize("rows,cols", [(64, 32000), (33, 1000), (5, 7)])
+@pytest.mark.parametrize("rows,cols", [(64, 32000), (33, 1000), (5, 7), (6, 200000)])
 def test_cfg2_softmax_argmax_matches_oracle(hip, dt, decomposed, rows, cols):
+    # (6, 200000): rows longer than the registers hold (800 KB in f32), re-read instead of cached
     print(f"cfg2 {dt.name} decomposed={decomposed} {rows}x{cols}", flush=True)
     g, x, y, a = softmax_graph(rows, cols, dt, decomposed)
     xv = randn([rows, cols], 21, 3.0)
@@ -95,14 +96,17 @@ def test_cfg2_softmax_argmax_matches_oracle(hip, dt, decomposed, rows, cols):
     np.testing.assert_array_equal(ga.numpy(), wa.numpy())
     assert ga.dtype == DType.I32
     if dt == DType.F32:
-        # The oracle folds the 32000-term row sum sequentially in f32 (interp/nn.rs:53-58), which
-        # alone carries ~1e-5..1e-4 relative error; the 1e-5 bar is therefore taken against the
-        # f64 softmax of the same inputs, and the oracle difference is bounded at 1e-4.
+        # The oracle folds the row sum sequentially in f32 (interp/nn.rs:53-58): for `cols`
+        # positive terms that carries up to (cols - 1) * 2^-24 relative error (first order),
+        # in practice a few per cent of it (2.9e-4 at 200000 columns). The 1e-5 bar is therefore
+        # taken against the f64 softmax of the same inputs, and the oracle difference is bounded
+        # at max(1e-4, 0.05 * cols * 2^-24) (1e-4 up to 32000 columns).
         x64 = xv.astype(np.float64)
         e = np.exp(x64 - x64.max(axis=1, keepdims=True))
         truth = e / e.sum(axis=1, keepdims=True)
         assert_close(to_f32(gy), truth, rtol=1e-5, atol=1e-30, what="softmax f32 vs f64")
-        assert_close(to_f32(gy), to_f32(wy), rtol=1e-4, atol=1e-30, what="softmax f32 vs oracle")
+        oracle_bar = max(1e-4, 0.05 * cols * 2.0**-24)
+        assert_close(to_f32(gy), to_f32(wy), rtol=oracle_bar, atol=1e-30, what="softmax f32 vs oracle")
     else:
         # elementwise: 1e-2 of each element plus one bf16 step at its own magnitude (the device
         # rounds at the same primitives as the oracle; only f32 fold orders differ)
