@@ -37,7 +37,7 @@ def cfg1_graph(n: int, m: int):
     return g, x, b, g.sum(h, 1)
 
 
-@pytest.mark.parametrize("n,m", [(64, 4096), (4096, 4096), (3, 100), (1, 7)])
+@pytest.mark.parametrize("n,m", [(64, 4096), (4096, 4096), (3, 100), (1, 7), (3, 300000)])
 def test_cfg1_fused_reduce_matches_oracle(hip, n, m):
     print(f"cfg1 n={n} m={m}", flush=True)
     g, x, b, y = cfg1_graph(n, m)
@@ -51,7 +51,9 @@ def test_cfg1_fused_reduce_matches_oracle(hip, n, m):
     truth = h.astype(np.float64).sum(axis=1)
     assert rel_err(got, truth) <= 1e-5
     assert_close(got, truth, rtol=1e-5, atol=1e-5 * np.abs(truth).max(), what="cfg1 vs f64")
-    assert_close(got, want, rtol=2e-5, atol=2e-5 * np.abs(want).max(), what="cfg1 vs oracle")
+    # the oracle's sequential f32 fold of m terms: up to (m - 1) * 2^-24 relative (first order)
+    bar = max(2e-5, 0.05 * m * 2.0**-24)
+    assert_close(got, want, rtol=bar, atol=bar * np.abs(want).max(), what="cfg1 vs oracle")
 
 
 def test_cfg1_is_one_kernel(hip):
